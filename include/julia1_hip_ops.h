@@ -1,0 +1,126 @@
+/*
+ * julia1_hip_ops.h — the individual gfx950 kernels of the encoder forward,
+ * callable on caller-owned device memory.
+ *
+ * These are the launch wrappers jh_forward uses, exported so each kernel can
+ * be parity-tested and timed on its own (the GEMM sweep runs through
+ * jh_op_gemm).  All pointers are device pointers; `stream` is a hipStream_t
+ * (NULL = the null stream).  Calls enqueue work and return; they do not
+ * synchronise.  Shape errors return JH_ERR_INVALID before anything is
+ * launched.  Element types: f32 = float, bf16 = uint16_t bit patterns.
+ *
+ * Each entry point names the reference kernel or library call it stands in
+ * for; the reference launches its own versions from src/cuda/mod.rs:400-521.
+ */
+#ifndef JULIA1_HIP_OPS_H
+#define JULIA1_HIP_OPS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Epilogues of jh_op_gemm: what happens to each FP32 accumulator tile of out = X · Wᵀ. */
+enum {
+    JH_EPI_STORE_BF16 = 0,      /* out bf16 = acc                                         */
+    JH_EPI_ROPE_BF16 = 1,       /* out bf16 = acc, rotate-half RoPE applied to the columns  */
+                                /*   below rope_cols (q and k of a packed qkv row)          */
+    JH_EPI_GEGLU_BF16 = 2,      /* W rows interleaved per 32 (see jh_op_interleave_geglu):  */
+                                /*   out[:, n/2] bf16 = gelu(gate) * up                     */
+    JH_EPI_RESID_F32 = 3,       /* out f32 += acc (+ bias if given)                         */
+    JH_EPI_BIAS_BF16 = 4,       /* out bf16 = acc + bias                                    */
+    JH_EPI_BIAS_RELU_BF16 = 5,  /* out bf16 = max(acc + bias, 0)                            */
+    JH_EPI_BIAS_F32 = 6         /* out f32 = acc + bias                                     */
+};
+
+/*
+ * out[r, col + n] = epi( Σ_k X[row(r), k] · W[n, k] ) for r < rows, n < N.
+ *  X bf16 with row stride ldx; row(r) = gather ? gather[r] : r.
+ *  W bf16 [N, K] row-major (PyTorch Linear layout).
+ *  out has row stride ldo (elements), written from column `col`.
+ *  bias f32 [N] (NULL allowed for RESID_F32).
+ *  ROPE: pos[r] is the row's position; cos/sin are [positions, 32] f32 tables;
+ *        columns < rope_cols are rotated per 64-wide head.
+ * Requirements: K % 64 == 0, N % 64 == 0, K <= 8192.  Replaces cuBLAS gemm_ex
+ * (src/cuda/mod.rs:347-375) plus the separate geglu/bias_act kernels
+ * (src/cuda/kernels.cu:137-172) and the residual add of ln_bf16 (:97-109).
+ */
+int jh_op_gemm(int epilogue, const void* x, size_t ldx, const int32_t* gather, size_t rows,
+               const void* w, size_t n, size_t k, void* out, size_t ldo, size_t col,
+               const float* bias, const int32_t* pos, const float* cos_t, const float* sin_t,
+               size_t rope_cols, void* stream);
+
+/* Reorder a host FP32 Wi [2*inter, k] into the gate/up interleave JH_EPI_GEGLU_BF16 expects. */
+void jh_op_interleave_geglu(const float* wi, size_t inter, size_t k, float* out);
+
+/*
+ * x[t] = LayerNorm(table[ids[t]]; w, no bias, eps) (f32), xn[t] = bf16(x[t]).
+ * table f32 [vocab, hidden].  Replaces embed_ln (src/cuda/kernels.cu:66-75).
+ */
+int jh_op_embed_ln(const uint32_t* ids, size_t rows, const float* table, const float* w,
+                   float eps, size_t hidden, float* x, void* xn, void* stream);
+
+/*
+ * out[r] = bf16(LayerNorm(x[r]; w, b, eps)), b may be NULL.
+ * Replaces ln_bf16 (src/cuda/kernels.cu:97-109) without its residual add,
+ * which the producing GEMM's RESID_F32 epilogue performs instead.
+ */
+int jh_op_layer_norm(const float* x, size_t rows, const float* w, const float* b, float eps,
+                     size_t hidden, void* out, void* stream);
+
+/*
+ * Encoder final norm fused with the question-type embedding and the first
+ * head layer's norm1: x[t] = LN(x[t]; fw, eps) + type_emb[qtype(t)];
+ * out[t] = bf16(LN(x[t]; hw, hb, 1e-5)).  tok_meta[t] packs the token's
+ * position (bits 0..15) and its sequence's qtype (bits 16..23).
+ * Replaces final_norm (src/cuda/kernels.cu:113-132).
+ */
+int jh_op_final_norm(float* x, size_t rows, const float* fw, const float* type_emb,
+                     const uint32_t* tok_meta, const float* hw, const float* hb, float eps,
+                     size_t hidden, void* out, void* stream);
+
+/*
+ * dst[r] = src[idx[r]] for f32 rows of `hidden`.  Replaces gather_rows
+ * (src/cuda/kernels.cu:175-183) for the FP32 residual; bf16 marker gathers
+ * are folded into jh_op_gemm's `gather` argument instead.
+ */
+int jh_op_gather_f32(const float* src, const int32_t* idx, size_t rows, size_t hidden,
+                     float* dst, void* stream);
+
+/*
+ * score[r] = Σ_i gelu(z[r, i]) · w2[i] + b2 (z already includes scorer.1's bias).
+ * Replaces scorer (src/cuda/kernels.cu:186-194).
+ */
+int jh_op_scorer(const float* z, size_t rows, size_t hidden, const float* w2, float b2,
+                 float* out, void* stream);
+
+/*
+ * Attention work item: `nq` query rows starting at absolute row `q_row` attend
+ * to `kv_len` key/value rows starting at `kv_row`; the first query sits at
+ * sequence position `q_pos` (keys are at positions 0..kv_len-1), which is what
+ * the sliding window measures against.  nq <= 64.
+ */
+typedef struct jh_attn_tile {
+    int32_t q_row, nq, kv_row, kv_len, q_pos;
+} jh_attn_tile;
+
+/*
+ * FlashAttention-2 forward, one workgroup per (tile, head): MFMA QKᵀ and PV,
+ * K/Vᵀ staged in LDS, online softmax of scale·QKᵀ over keys with
+ * |q_pos - k_pos| <= window (window < 0: all keys of the sequence).
+ * q/k/v bf16 with row strides ldq/ldkv; head h reads columns [64h, 64h+64)
+ * of each; out bf16 row stride ldo.  `tiles` is a device array.
+ * Replaces attention_rope/attention_plain (src/cuda/kernels.cu:274-391); RoPE
+ * is applied by the producing GEMM's ROPE epilogue instead of on every load.
+ */
+int jh_op_attention(const void* q, size_t ldq, const void* k, const void* v, size_t ldkv,
+                    void* out, size_t ldo, const jh_attn_tile* tiles, size_t ntiles,
+                    size_t heads, int window, float scale, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* JULIA1_HIP_OPS_H */

@@ -1,0 +1,214 @@
+// FlashAttention-2 forward for gfx950: one workgroup of two waves per
+// (64-query tile, head); each wave owns 32 queries.
+//
+// The score tile is computed transposed, Sᵀ = K·Qᵀ, with
+// v_mfma_f32_32x32x16_bf16 (M = 32 keys, N = 32 queries, K = 16 head dims).
+// The accumulator layout then gives every lane ONE query (column l%32) and
+// 16 of its keys, the other 16 sitting in lane l^32 — so the online-softmax
+// state (running max m, running sum l) is one scalar per lane and each row
+// reduction is a single cross-half exchange.  The output is also produced
+// transposed, Oᵀ = Vᵀ·Pᵀ: Pᵀ as the MFMA B operand needs, per lane, that same
+// query and 8 keys, which are exactly 8 of the Sᵀ accumulator values the lane
+// already holds (the MFMA's K order is a permutation of keys; Vᵀ is read in
+// the same permutation).  P therefore never leaves registers.
+//
+// K tiles (64 keys x 64 dims) are staged row-major in LDS (stride 72 bf16:
+// conflict-free 16-byte fragment reads); V tiles are staged transposed
+// (Vᵀ[dim][key], stride 68 bf16: conflict-free 8-byte reads), both double
+// buffered with register prefetch.  Sliding-window tiles only visit keys in
+// [q_pos - window, q_pos + nq - 1 + window] ∩ [0, kv_len), with per-element
+// masking of |q - k| <= window inside the band.
+#include <hip/hip_runtime.h>
+
+#include "kernels.hpp"
+
+namespace {
+
+constexpr int KT = 64;       // keys per LDS tile
+constexpr int KSTR = 72;     // K tile row stride (bf16)
+constexpr int VSTR = 68;     // Vᵀ tile row stride (bf16)
+constexpr int NTHR = 128;
+
+__global__ __launch_bounds__(NTHR) void attention_kernel(AttnArgs a) {
+    __shared__ __align__(16) bf16_t sK[2][KT][KSTR];
+    __shared__ __align__(16) bf16_t sV[2][64][VSTR];
+
+    const AttnTile tile = a.tiles[blockIdx.x];
+    const int head = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lq = lane & 31, g = lane >> 5;
+
+    const bf16_t* kbase = a.k + (long)tile.kv_row * a.ldkv + head * 64;
+    const bf16_t* vbase = a.v + (long)tile.kv_row * a.ldkv + head * 64;
+
+    // Q fragments (B operand of Sᵀ = K·Qᵀ): query lq of this wave, dims ks*16 + 8g .. +7.
+    const int qi = wave * 32 + lq;  // query index within the tile
+    bf16x8 qf[4];
+    {
+        const bool ok = qi < tile.nq;
+        const bf16_t* qp = a.q + (long)(tile.q_row + (ok ? qi : 0)) * a.ldq + head * 64 + g * 8;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            u32x4 r = ok ? *(const u32x4*)(qp + ks * 16) : u32x4{0, 0, 0, 0};
+            qf[ks] = __builtin_bit_cast(bf16x8, r);
+        }
+    }
+    const int qpos = tile.q_pos + qi;
+
+    int kbeg = 0, kend = tile.kv_len;
+    if (a.window >= 0) {
+        kbeg = max(0, tile.q_pos - a.window);
+        kend = min(tile.kv_len, tile.q_pos + tile.nq + a.window);
+    }
+
+    // Global->register staging of one K/V tile: K as 4 16-byte chunks per
+    // thread; V as 2 (key pair x 8 dims) units per thread.
+    u32x4 rk[4], rv[2][2];
+    auto gload = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            int c = tid + NTHR * i, key = c >> 3, dc = c & 7;
+            rk[i] = k0 + key < kend ? *(const u32x4*)(kbase + (long)(k0 + key) * a.ldkv + dc * 8) : u32x4{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            int u = tid + NTHR * i, pr = u & 31, dc = u >> 5;
+            int key = k0 + 2 * pr;
+            rv[i][0] = key < kend ? *(const u32x4*)(vbase + (long)key * a.ldkv + dc * 8) : u32x4{0, 0, 0, 0};
+            rv[i][1] = key + 1 < kend ? *(const u32x4*)(vbase + (long)(key + 1) * a.ldkv + dc * 8) : u32x4{0, 0, 0, 0};
+        }
+    };
+    auto sstore = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            int c = tid + NTHR * i;
+            *(u32x4*)&sK[buf][c >> 3][(c & 7) * 8] = rk[i];
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            int u = tid + NTHR * i, pr = u & 31, dc = u >> 5;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                uint32_t a0 = rv[i][0][w], a1 = rv[i][1][w];
+                // dims dc*8 + 2w (low halves) and dc*8 + 2w + 1 (high halves); keys 2pr, 2pr+1
+                *(uint32_t*)&sV[buf][dc * 8 + 2 * w][2 * pr] = (a0 & 0xffffu) | (a1 << 16);
+                *(uint32_t*)&sV[buf][dc * 8 + 2 * w + 1][2 * pr] = (a0 >> 16) | (a1 & 0xffff0000u);
+            }
+        }
+    };
+
+    f32x16 o[2];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) o[0][e] = o[1][e] = 0.0f;
+    float m = -INFINITY, l = 0.0f;
+    const float sl2 = a.scale_log2;
+
+    const int ntk = kend > kbeg ? (kend - kbeg + KT - 1) / KT : 0;
+    if (ntk > 0) {
+        gload(kbeg);
+        sstore(0);
+    }
+    __syncthreads();
+    for (int it = 0; it < ntk; ++it) {
+        const int buf = it & 1, k0 = kbeg + it * KT;
+        if (it + 1 < ntk) gload(k0 + KT);
+
+        // Sᵀ for keys [k0, k0+64): two 32-key blocks.
+        f32x16 s[2];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) s[kb][e] = 0.0f;
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                bf16x8 kf = *(const bf16x8*)&sK[buf][kb * 32 + lq][ks * 16 + g * 8];
+                s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], s[kb], 0, 0, 0);
+            }
+        }
+        // Mask + scale; element e of block kb is key k0 + kb*32 + (e/4)*8 + 4g + e%4.
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                int key = k0 + kb * 32 + (e >> 2) * 8 + g * 4 + (e & 3);
+                bool ok = key < kend && (a.window < 0 || abs(qpos - key) <= a.window);
+                float v = ok ? s[kb][e] * sl2 : -INFINITY;
+                s[kb][e] = v;
+                mx = fmaxf(mx, v);
+            }
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float mn = fmaxf(m, mx);
+        const float u = mn == -INFINITY ? 0.0f : mn;
+        const float alpha = __builtin_amdgcn_exp2f(m - u);
+        m = mn;
+        float ls = 0.0f;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                float p = __builtin_amdgcn_exp2f(s[kb][e] - u);
+                s[kb][e] = p;
+                ls += p;
+            }
+        l = l * alpha + ls;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            o[0][e] *= alpha;
+            o[1][e] *= alpha;
+        }
+        // Oᵀ += Vᵀ·Pᵀ over 4 steps of 16 keys.  Step (kb, hb) uses accumulator
+        // elements hb*8 .. hb*8+7 of block kb: keys base + 8*(e/4) + 4g + e%4.
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int hb = 0; hb < 2; ++hb) {
+                bf16x8 pf;
+                {
+                    u32x4 r;
+#pragma unroll
+                    for (int w = 0; w < 4; ++w) r[w] = pack2(s[kb][hb * 8 + 2 * w], s[kb][hb * 8 + 2 * w + 1]);
+                    pf = __builtin_bit_cast(bf16x8, r);
+                }
+                const int base = kb * 32 + hb * 16 + g * 4;
+#pragma unroll
+                for (int db = 0; db < 2; ++db) {
+                    const bf16_t* vr = &sV[buf][db * 32 + lq][0];
+                    u32x2 lo = *(const u32x2*)(vr + base);
+                    u32x2 hi = *(const u32x2*)(vr + base + 8);
+                    bf16x8 vf = __builtin_bit_cast(bf16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+                    o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, o[db], 0, 0, 0);
+                }
+            }
+        if (it + 1 < ntk) sstore(buf ^ 1);
+        __syncthreads();
+    }
+
+    l += __shfl_xor(l, 32, 64);
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    if (qi < tile.nq) {
+        bf16_t* op = a.out + (long)(tile.q_row + qi) * a.ldo + head * 64;
+#pragma unroll
+        for (int db = 0; db < 2; ++db)
+#pragma unroll
+            for (int qd = 0; qd < 4; ++qd) {
+                int d = db * 32 + qd * 8 + g * 4;
+                *(u32x2*)(op + d) = u32x2{pack2(o[db][qd * 4] * inv, o[db][qd * 4 + 1] * inv),
+                                          pack2(o[db][qd * 4 + 2] * inv, o[db][qd * 4 + 3] * inv)};
+            }
+    }
+}
+
+}  // namespace
+
+void launch_attention(const AttnArgs& a, hipStream_t s) {
+    if (a.ntiles < 0 || a.heads <= 0) throw jh_error(1, "attention: bad tile/head count");
+    if (a.ntiles == 0) return;
+    if (!a.q || !a.k || !a.v || !a.out || !a.tiles) throw jh_error(1, "attention: null operand");
+    if (a.ldq % 8 || a.ldkv % 8 || a.ldo % 4 || a.ldq < a.heads * 64 || a.ldo < a.heads * 64 ||
+        ((uintptr_t)a.q & 15) || ((uintptr_t)a.k & 15) || ((uintptr_t)a.v & 15) || ((uintptr_t)a.out & 7))
+        throw jh_error(1, "attention: operands must be 16-byte aligned with row strides % 8 == 0");
+    if (a.ntiles > 0x7fffffff || a.heads > 65535) throw jh_error(1, "attention: grid too large");
+    hipLaunchKernelGGL(attention_kernel, dim3(a.ntiles, a.heads), dim3(NTHR), 0, s, a);
+    HIP_CHECK(hipGetLastError());
+}

@@ -1,0 +1,624 @@
+// The HIP backend model: device-resident BF16 weights, a grow-only
+// workspace, batch staging, and the encoder-forward launch sequence.
+// Replaces CudaModel (src/cuda/mod.rs) behind the C-ABI of julia1_hip.h.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/julia1_hip.h"
+#include "../../include/julia1_hip_ops.h"
+#include "abi_util.hpp"
+#include "kernels.hpp"
+
+namespace {
+
+struct DevBuf {
+    void* p = nullptr;
+    size_t bytes = 0;
+    DevBuf() = default;
+    DevBuf(const DevBuf&) = delete;
+    DevBuf& operator=(const DevBuf&) = delete;
+    DevBuf(DevBuf&& o) noexcept : p(o.p), bytes(o.bytes) { o.p = nullptr; o.bytes = 0; }
+    DevBuf& operator=(DevBuf&& o) noexcept {
+        if (this != &o) { release(); p = o.p; bytes = o.bytes; o.p = nullptr; o.bytes = 0; }
+        return *this;
+    }
+    ~DevBuf() { release(); }
+    void alloc(size_t n) {
+        release();
+        if (hipMalloc(&p, std::max<size_t>(n, 256)) != hipSuccess) {
+            p = nullptr;
+            (void)hipGetLastError();
+            throw jh_error(JH_ERR_ALLOC, "hipMalloc of " + std::to_string(n) + " bytes failed");
+        }
+        bytes = n;
+    }
+    void release() {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        bytes = 0;
+    }
+    template <class T> T* as() const { return (T*)p; }
+};
+
+struct PinnedBuf {
+    void* p = nullptr;
+    size_t bytes = 0;
+    PinnedBuf() = default;
+    PinnedBuf(const PinnedBuf&) = delete;
+    PinnedBuf& operator=(const PinnedBuf&) = delete;
+    ~PinnedBuf() { release(); }
+    void alloc(size_t n) {
+        release();
+        if (hipHostMalloc(&p, std::max<size_t>(n, 256), hipHostMallocDefault) != hipSuccess) {
+            p = nullptr;
+            (void)hipGetLastError();
+            throw jh_error(JH_ERR_ALLOC, "hipHostMalloc of " + std::to_string(n) + " bytes failed");
+        }
+        bytes = n;
+    }
+    void release() {
+        if (p) (void)hipHostFree(p);
+        p = nullptr;
+        bytes = 0;
+    }
+    template <class T> T* as() const { return (T*)p; }
+};
+
+DevBuf upload_bytes(const void* src, size_t bytes) {
+    DevBuf b;
+    b.alloc(bytes);
+    HIP_CHECK(hipMemcpy(b.p, src, bytes, hipMemcpyHostToDevice));
+    return b;
+}
+
+DevBuf upload_f32(const float* src, size_t n) {
+    if (!src) throw jh_error(JH_ERR_INVALID, "missing weight tensor");
+    return upload_bytes(src, n * sizeof(float));
+}
+
+// FP32 -> BF16 (round to nearest even) on the host, then upload (half::bf16::from_f32, src/cuda/mod.rs:36-39).
+DevBuf upload_bf16(const float* src, size_t n) {
+    if (!src) throw jh_error(JH_ERR_INVALID, "missing weight tensor");
+    std::vector<bf16_t> tmp(n);
+    for (size_t i = 0; i < n; ++i) tmp[i] = f2bf(src[i]);
+    return upload_bytes(tmp.data(), n * sizeof(bf16_t));
+}
+
+struct EncLayer {
+    DevBuf attn_norm, wqkv, wo, mlp_norm, wi, wo2;
+    int rope = 0;
+    bool global = false;
+};
+
+struct HeadLayer {
+    DevBuf norm1_w, norm1_b, in_w, in_b, out_w, out_b, norm2_w, norm2_b, lin1_w, lin1_b, lin2_w, lin2_b;
+};
+
+constexpr int QTILE = 64;  // queries per attention work item
+
+}  // namespace
+
+struct jh_model {
+    std::mutex mu;
+    int device = 0;
+    hipStream_t stream = nullptr;
+    // configuration
+    int h = 0, heads = 0, inter = 0, nlayers = 0, half_window = 0, vocab = 0, max_pos = 0, head_heads = 0, ff = 0;
+    float eps = 1e-5f;
+    // weights
+    DevBuf emb, emb_norm, final_norm, type_emb, s_norm_w, s_norm_b, s_w1, s_b1, s_w2;
+    float s_b2 = 0.0f;
+    std::vector<EncLayer> layers;
+    std::vector<HeadLayer> head;
+    std::vector<std::pair<DevBuf, DevBuf>> ropes;
+    // workspace (grow-only)
+    size_t cap_t = 0, cap_m = 0, cap_meta = 0;
+    uint64_t ws_gen = 0;
+    DevBuf x, xn, qkv, ctx, hbuf, y, yn, qm, cm, hm, z, scores, meta;
+    PinnedBuf meta_host, scores_host;
+    // staged batch
+    bool staged = false;
+    size_t T = 0, S = 0, M = 0, ntiles = 0, nmtiles = 0;
+    uint32_t* d_ids = nullptr;
+    uint32_t* d_tok = nullptr;
+    AttnTile* d_tiles = nullptr;
+    AttnTile* d_mtiles = nullptr;
+    int32_t* d_markers = nullptr;
+    // graph of the launch sequence for the staged shape
+    bool use_graph = true;
+    hipGraphExec_t graph = nullptr;
+    size_t graph_key[6] = {0, 0, 0, 0, 0, 0};
+    std::string name;
+
+    ~jh_model() {
+        if (graph) (void)hipGraphExecDestroy(graph);
+        if (stream) (void)hipStreamDestroy(stream);
+    }
+
+    void bind() const { HIP_CHECK(hipSetDevice(device)); }
+
+    void ensure_workspace(size_t t, size_t m, size_t meta_len) {
+        if (t > cap_t || m > cap_m) {
+            size_t ct = 1024, cm_ = 256;
+            while (ct < std::max(t, cap_t)) ct <<= 1;
+            while (cm_ < std::max(m, cap_m)) cm_ <<= 1;
+            size_t H = h, wide = std::max<size_t>(inter, ff);
+            x.alloc(ct * H * 4);
+            xn.alloc(ct * H * 2);
+            qkv.alloc(ct * 3 * H * 2);
+            ctx.alloc(ct * H * 2);
+            hbuf.alloc(ct * wide * 2);
+            y.alloc(cm_ * H * 4);
+            yn.alloc(cm_ * H * 2);
+            qm.alloc(cm_ * H * 2);
+            this->cm.alloc(cm_ * H * 2);
+            hm.alloc(cm_ * ff * 2);
+            z.alloc(cm_ * H * 4);
+            scores.alloc(cm_ * 4);
+            scores_host.alloc(cm_ * 4);
+            cap_t = ct;
+            cap_m = cm_;
+            ++ws_gen;
+        }
+        if (meta_len > cap_meta) {
+            size_t n = 4096;
+            while (n < meta_len) n <<= 1;
+            meta.alloc(n * 4);
+            meta_host.alloc(n * 4);
+            cap_meta = n;
+            ++ws_gen;
+        }
+    }
+
+    // Validates and uploads a packed batch (Batch, src/model.rs:114-124).
+    void stage(const uint32_t* ids, size_t t, const uint32_t* starts, const uint32_t* lens, const uint8_t* qtypes,
+               size_t nseq, const uint32_t* marker_rows, size_t m) {
+        if ((t && !ids) || (nseq && (!starts || !lens || !qtypes)) || (m && !marker_rows))
+            throw jh_error(JH_ERR_INVALID, "null batch array");
+        if (t > (size_t)0x7fffffff || m > (size_t)0x7fffffff) throw jh_error(JH_ERR_INVALID, "batch too large");
+        size_t next = 0;
+        for (size_t s = 0; s < nseq; ++s) {
+            if (starts[s] != next) throw jh_error(JH_ERR_INVALID, "sequences must be packed back to back in order");
+            if (lens[s] > (uint32_t)max_pos)
+                throw jh_error(JH_ERR_INVALID, "sequence longer than max_position_embeddings");
+            if (qtypes[s] > 2) throw jh_error(JH_ERR_INVALID, "qtype must be 0, 1 or 2");
+            next += lens[s];
+        }
+        if (next != t) throw jh_error(JH_ERR_INVALID, "sequence lengths do not sum to the token count");
+        for (size_t i = 0; i < t; ++i)
+            if (ids[i] >= (uint32_t)vocab) throw jh_error(JH_ERR_INVALID, "token id out of vocabulary");
+        // Attention work items: 64-query tiles per sequence; marker tiles per sequence.
+        std::vector<AttnTile> tiles, mtiles;
+        for (size_t s = 0; s < nseq; ++s)
+            for (uint32_t q0 = 0; q0 < lens[s]; q0 += QTILE)
+                tiles.push_back({(int32_t)(starts[s] + q0), (int32_t)std::min<uint32_t>(QTILE, lens[s] - q0),
+                                 (int32_t)starts[s], (int32_t)lens[s], (int32_t)q0});
+        size_t mi = 0;
+        for (size_t s = 0; s < nseq; ++s) {
+            size_t first = mi;
+            while (mi < m && marker_rows[mi] >= starts[s] && marker_rows[mi] < starts[s] + lens[s]) ++mi;
+            for (size_t j = first; j < mi; j += QTILE)
+                mtiles.push_back({(int32_t)j, (int32_t)std::min<size_t>(QTILE, mi - j), (int32_t)starts[s],
+                                  (int32_t)lens[s], 0});
+        }
+        if (mi != m) throw jh_error(JH_ERR_INVALID, "marker rows must lie in their sequence, grouped by sequence");
+        const size_t meta_len = 2 * t + 5 * (tiles.size() + mtiles.size()) + m;
+        ensure_workspace(t, m, meta_len);
+        // The previous upload may still be reading the pinned staging buffer.
+        HIP_CHECK(hipStreamSynchronize(stream));
+        uint32_t* hm_ = meta_host.as<uint32_t>();
+        std::memcpy(hm_, ids, t * 4);
+        uint32_t* tok = hm_ + t;
+        for (size_t s = 0; s < nseq; ++s)
+            for (uint32_t i = 0; i < lens[s]; ++i) tok[starts[s] + i] = i | ((uint32_t)qtypes[s] << 16);
+        std::memcpy(hm_ + 2 * t, tiles.data(), tiles.size() * sizeof(AttnTile));
+        std::memcpy(hm_ + 2 * t + 5 * tiles.size(), mtiles.data(), mtiles.size() * sizeof(AttnTile));
+        std::memcpy(hm_ + 2 * t + 5 * (tiles.size() + mtiles.size()), marker_rows, m * 4);
+        HIP_CHECK(hipMemcpyAsync(meta.p, meta_host.p, meta_len * 4, hipMemcpyHostToDevice, stream));
+        uint32_t* dm = meta.as<uint32_t>();
+        d_ids = dm;
+        d_tok = dm + t;
+        d_tiles = (AttnTile*)(dm + 2 * t);
+        d_mtiles = (AttnTile*)(dm + 2 * t + 5 * tiles.size());
+        d_markers = (int32_t*)(dm + 2 * t + 5 * (tiles.size() + mtiles.size()));
+        T = t;
+        S = nseq;
+        M = m;
+        ntiles = tiles.size();
+        nmtiles = mtiles.size();
+        staged = true;
+    }
+
+    void gemm(int epi, const void* xp, long ldx, const int32_t* gather, size_t rows, const DevBuf& w, int n, int k,
+              void* out, long ldo, int col, const float* bias, const float* cos_t = nullptr,
+              const float* sin_t = nullptr, int rope_cols = 0) {
+        GemmArgs a{(const bf16_t*)xp, ldx, gather, (int)rows, w.as<bf16_t>(), n, k, out, ldo, col, bias,
+                   (const int32_t*)d_tok, cos_t, sin_t, rope_cols};
+        launch_gemm(epi, a, stream);
+    }
+
+    void attention(const bf16_t* q, long ldq, const bf16_t* k, const bf16_t* v, long ldkv, bf16_t* out, long ldo,
+                   const AttnTile* tiles, size_t n, int nheads, int window) {
+        AttnArgs a{q, ldq, k, v, ldkv, out, ldo, tiles, (int)n, nheads, window, 0.125f * 1.4426950408889634f};
+        launch_attention(a, stream);
+    }
+
+    // Embeddings and the first `upto` encoder layers (src/cuda/mod.rs:446-463).
+    void run_encoder(int upto) {
+        const int H = h;
+        const size_t t = T;
+        launch_embed_ln(d_ids, (int)t, emb.as<float>(), emb_norm.as<float>(), eps, H, x.as<float>(), xn.as<bf16_t>(),
+                        stream);
+        for (int l = 0; l < upto; ++l) {
+            EncLayer& L = layers[l];
+            if (L.attn_norm.p)
+                launch_layer_norm(x.as<float>(), (int)t, L.attn_norm.as<float>(), nullptr, eps, H, xn.as<bf16_t>(),
+                                  stream);
+            gemm(JH_EPI_ROPE_BF16, xn.p, H, nullptr, t, L.wqkv, 3 * H, H, qkv.p, 3 * H, 0, nullptr,
+                 ropes[L.rope].first.as<float>(), ropes[L.rope].second.as<float>(), 2 * H);
+            const bf16_t* q = qkv.as<bf16_t>();
+            attention(q, 3 * H, q + H, q + 2 * H, 3 * H, ctx.as<bf16_t>(), H, d_tiles, ntiles, heads,
+                      L.global ? -1 : half_window);
+            gemm(JH_EPI_RESID_F32, ctx.p, H, nullptr, t, L.wo, H, H, x.p, H, 0, nullptr);
+            launch_layer_norm(x.as<float>(), (int)t, L.mlp_norm.as<float>(), nullptr, eps, H, xn.as<bf16_t>(), stream);
+            gemm(JH_EPI_GEGLU_BF16, xn.p, H, nullptr, t, L.wi, 2 * inter, H, hbuf.p, inter, 0, nullptr);
+            gemm(JH_EPI_RESID_F32, hbuf.p, inter, nullptr, t, L.wo2, H, inter, x.p, H, 0, nullptr);
+        }
+    }
+
+    // Final norm, decision head and scorer (src/cuda/mod.rs:464-511; the last head
+    // layer computes queries and FFN for markers only, as src/cpu/mod.rs:287-321).
+    void run_head() {
+        const int H = h;
+        const size_t t = T, m = M;
+        const int nh = (int)head.size();
+        launch_final_norm(x.as<float>(), (int)t, final_norm.as<float>(), type_emb.as<float>(), d_tok,
+                          head[0].norm1_w.as<float>(), head[0].norm1_b.as<float>(), eps, H, xn.as<bf16_t>(), stream);
+        for (int j = 0; j + 1 < nh; ++j) {
+            HeadLayer& L = head[j];
+            gemm(JH_EPI_BIAS_BF16, xn.p, H, nullptr, t, L.in_w, 3 * H, H, qkv.p, 3 * H, 0, L.in_b.as<float>());
+            const bf16_t* q = qkv.as<bf16_t>();
+            attention(q, 3 * H, q + H, q + 2 * H, 3 * H, ctx.as<bf16_t>(), H, d_tiles, ntiles, head_heads, -1);
+            gemm(JH_EPI_RESID_F32, ctx.p, H, nullptr, t, L.out_w, H, H, x.p, H, 0, L.out_b.as<float>());
+            launch_layer_norm(x.as<float>(), (int)t, L.norm2_w.as<float>(), L.norm2_b.as<float>(), 1e-5f, H,
+                              xn.as<bf16_t>(), stream);
+            gemm(JH_EPI_BIAS_RELU_BF16, xn.p, H, nullptr, t, L.lin1_w, ff, H, hbuf.p, ff, 0, L.lin1_b.as<float>());
+            gemm(JH_EPI_RESID_F32, hbuf.p, ff, nullptr, t, L.lin2_w, H, ff, x.p, H, 0, L.lin2_b.as<float>());
+            HeadLayer& N = head[j + 1];
+            launch_layer_norm(x.as<float>(), (int)t, N.norm1_w.as<float>(), N.norm1_b.as<float>(), 1e-5f, H,
+                              xn.as<bf16_t>(), stream);
+        }
+        HeadLayer& L = head[nh - 1];
+        // Keys/values for every token: in_proj rows [H, 3H) into qkv columns [H, 3H).
+        {
+            GemmArgs a{xn.as<bf16_t>(), H, nullptr, (int)t, L.in_w.as<bf16_t>() + (size_t)H * H, 2 * H, H, qkv.p,
+                       3 * H, H, L.in_b.as<float>() + H, nullptr, nullptr, nullptr, 0};
+            launch_gemm(JH_EPI_BIAS_BF16, a, stream);
+        }
+        // Queries for markers only, gathered straight from the normed rows.
+        gemm(JH_EPI_BIAS_BF16, xn.p, H, d_markers, m, L.in_w, H, H, qm.p, H, 0, L.in_b.as<float>());
+        const bf16_t* kv = qkv.as<bf16_t>();
+        attention(qm.as<bf16_t>(), H, kv + H, kv + 2 * H, 3 * H, cm.as<bf16_t>(), H, d_mtiles, nmtiles, head_heads, -1);
+        launch_gather_f32(x.as<float>(), d_markers, (int)m, H, y.as<float>(), stream);
+        gemm(JH_EPI_RESID_F32, cm.p, H, nullptr, m, L.out_w, H, H, y.p, H, 0, L.out_b.as<float>());
+        launch_layer_norm(y.as<float>(), (int)m, L.norm2_w.as<float>(), L.norm2_b.as<float>(), 1e-5f, H,
+                          yn.as<bf16_t>(), stream);
+        gemm(JH_EPI_BIAS_RELU_BF16, yn.p, H, nullptr, m, L.lin1_w, ff, H, hm.p, ff, 0, L.lin1_b.as<float>());
+        gemm(JH_EPI_RESID_F32, hm.p, ff, nullptr, m, L.lin2_w, H, ff, y.p, H, 0, L.lin2_b.as<float>());
+        // Scorer: LayerNorm -> Linear -> GELU -> Linear(.., 1).
+        launch_layer_norm(y.as<float>(), (int)m, s_norm_w.as<float>(), s_norm_b.as<float>(), 1e-5f, H,
+                          yn.as<bf16_t>(), stream);
+        gemm(JH_EPI_BIAS_F32, yn.p, H, nullptr, m, s_w1, H, H, z.p, H, 0, s_b1.as<float>());
+        launch_scorer(z.as<float>(), (int)m, H, s_w2.as<float>(), s_b2, scores.as<float>(), stream);
+    }
+
+    void run_all() {
+        if (T == 0 || M == 0) return;
+        run_encoder(nlayers);
+        run_head();
+    }
+
+    void execute() {
+        if (!staged) throw jh_error(JH_ERR_INVALID, "no batch staged");
+        if (T == 0 || M == 0) return;
+        if (!use_graph) {
+            run_all();
+            return;
+        }
+        const size_t key[6] = {T, M, S, ntiles, nmtiles, (size_t)ws_gen};
+        if (!graph || !std::equal(key, key + 6, graph_key)) {
+            if (graph) {
+                (void)hipGraphExecDestroy(graph);
+                graph = nullptr;
+            }
+            HIP_CHECK(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
+            try {
+                run_all();
+            } catch (...) {
+                hipGraph_t g = nullptr;
+                (void)hipStreamEndCapture(stream, &g);
+                if (g) (void)hipGraphDestroy(g);
+                throw;
+            }
+            hipGraph_t g = nullptr;
+            HIP_CHECK(hipStreamEndCapture(stream, &g));
+            hipError_t e = hipGraphInstantiate(&graph, g, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(g);
+            if (e != hipSuccess) {
+                graph = nullptr;
+                throw jh_error(JH_ERR_DEVICE, std::string("hipGraphInstantiate: ") + hipGetErrorString(e));
+            }
+            std::copy(key, key + 6, graph_key);
+        }
+        HIP_CHECK(hipGraphLaunch(graph, stream));
+    }
+
+    void read_scores(float* out, size_t m) {
+        if (!staged) throw jh_error(JH_ERR_INVALID, "no batch staged");
+        if (m != M) throw jh_error(JH_ERR_INVALID, "score count does not match the staged markers");
+        if (m == 0) {
+            HIP_CHECK(hipStreamSynchronize(stream));
+            return;
+        }
+        HIP_CHECK(hipMemcpyAsync(scores_host.p, scores.p, m * 4, hipMemcpyDeviceToHost, stream));
+        HIP_CHECK(hipStreamSynchronize(stream));
+        std::memcpy(out, scores_host.p, m * 4);
+    }
+};
+
+namespace {
+
+void check_config(const jh_config* c) {
+    if (!c) throw jh_error(JH_ERR_INVALID, "null config");
+    if (c->head_dim != 64) throw jh_error(JH_ERR_INVALID, "kernels require head_dim 64");
+    if (c->hidden == 0 || c->hidden % 64 || c->hidden > 1024 || c->heads * 64 != c->hidden)
+        throw jh_error(JH_ERR_INVALID, "hidden must be heads*64 and at most 1024");
+    if (c->head_heads * 64 != c->hidden) throw jh_error(JH_ERR_INVALID, "head_heads must be hidden/64");
+    if (c->intermediate == 0 || c->intermediate % 64) throw jh_error(JH_ERR_INVALID, "intermediate must be a multiple of 64");
+    if (c->head_ff == 0 || c->head_ff % 64) throw jh_error(JH_ERR_INVALID, "head_ff must be a multiple of 64");
+    if (c->head_layers < 1) throw jh_error(JH_ERR_INVALID, "at least one head layer is required");
+    if (c->layers > 0 && (!c->global || !c->rope_theta)) throw jh_error(JH_ERR_INVALID, "missing per-layer config");
+    if (c->max_positions == 0 || c->max_positions > 65535) throw jh_error(JH_ERR_INVALID, "max_positions must be 1..65535");
+    if (c->vocab == 0) throw jh_error(JH_ERR_INVALID, "empty vocabulary");
+    if (c->half_window > 65535) throw jh_error(JH_ERR_INVALID, "half_window too large");
+}
+
+// Gate/up interleave for the GEGLU epilogue: 64-row block j holds gate rows
+// [32j, 32j+32) then up rows [inter+32j, inter+32j+32).
+void interleave_geglu(const float* wi, size_t inter, size_t k, float* out) {
+    for (size_t j = 0; j < inter / 32; ++j)
+        for (size_t r = 0; r < 32; ++r) {
+            std::memcpy(out + ((64 * j) + r) * k, wi + (32 * j + r) * k, k * sizeof(float));
+            std::memcpy(out + ((64 * j) + 32 + r) * k, wi + (inter + 32 * j + r) * k, k * sizeof(float));
+        }
+}
+
+void build_model(jh_model* m, const jh_config* c, const jh_weights* w, int ordinal) {
+    check_config(c);
+    if (!w || !w->embedding || !w->layers || !w->head) throw jh_error(JH_ERR_INVALID, "null weights");
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) {
+        (void)hipGetLastError();
+        throw jh_error(JH_ERR_DEVICE, "HIP device unavailable");
+    }
+    if (ordinal < 0 || ordinal >= count) throw jh_error(JH_ERR_DEVICE, "HIP device ordinal out of range");
+    m->device = ordinal;
+    m->bind();
+    hipDeviceProp_t prop;
+    HIP_CHECK(hipGetDeviceProperties(&prop, ordinal));
+    m->name = "hip:" + std::to_string(ordinal) + " (" + prop.name + ")";
+    HIP_CHECK(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking));
+    const size_t H = c->hidden, I = c->intermediate, F = c->head_ff;
+    m->h = (int)H; m->heads = (int)c->heads; m->inter = (int)I; m->nlayers = (int)c->layers;
+    m->half_window = (int)c->half_window; m->vocab = (int)c->vocab; m->max_pos = (int)c->max_positions;
+    m->head_heads = (int)c->head_heads; m->ff = (int)F; m->eps = c->norm_eps;
+    m->emb = upload_f32(w->embedding, (size_t)c->vocab * H);
+    m->emb_norm = upload_f32(w->emb_norm, H);
+    std::vector<float> thetas;
+    std::vector<float> wi_tmp(2 * I * H);
+    for (uint32_t l = 0; l < c->layers; ++l) {
+        const jh_encoder_layer& s = w->layers[l];
+        EncLayer L;
+        if (l > 0 && !s.attn_norm) throw jh_error(JH_ERR_INVALID, "encoder layers after the first need attn_norm");
+        if (s.attn_norm) L.attn_norm = upload_f32(s.attn_norm, H);
+        L.wqkv = upload_bf16(s.wqkv, 3 * H * H);
+        L.wo = upload_bf16(s.wo, H * H);
+        L.mlp_norm = upload_f32(s.mlp_norm, H);
+        if (!s.wi) throw jh_error(JH_ERR_INVALID, "missing Wi");
+        interleave_geglu(s.wi, I, H, wi_tmp.data());
+        L.wi = upload_bf16(wi_tmp.data(), 2 * I * H);
+        L.wo2 = upload_bf16(s.wo2, H * I);
+        L.global = c->global[l] != 0;
+        const float th = c->rope_theta[l];
+        auto it = std::find(thetas.begin(), thetas.end(), th);
+        if (it == thetas.end()) {
+            std::vector<float> cs((size_t)c->max_positions * 32), sn((size_t)c->max_positions * 32);
+            jh_rope_table(th, 64, c->max_positions, cs.data(), sn.data());
+            m->ropes.emplace_back(upload_f32(cs.data(), cs.size()), upload_f32(sn.data(), sn.size()));
+            thetas.push_back(th);
+            L.rope = (int)thetas.size() - 1;
+        } else {
+            L.rope = (int)(it - thetas.begin());
+        }
+        m->layers.push_back(std::move(L));
+    }
+    m->final_norm = upload_f32(w->final_norm, H);
+    m->type_emb = upload_f32(w->type_emb, 3 * H);
+    for (uint32_t l = 0; l < c->head_layers; ++l) {
+        const jh_head_layer& s = w->head[l];
+        HeadLayer L;
+        L.norm1_w = upload_f32(s.norm1_w, H); L.norm1_b = upload_f32(s.norm1_b, H);
+        L.in_w = upload_bf16(s.in_w, 3 * H * H); L.in_b = upload_f32(s.in_b, 3 * H);
+        L.out_w = upload_bf16(s.out_w, H * H); L.out_b = upload_f32(s.out_b, H);
+        L.norm2_w = upload_f32(s.norm2_w, H); L.norm2_b = upload_f32(s.norm2_b, H);
+        L.lin1_w = upload_bf16(s.lin1_w, F * H); L.lin1_b = upload_f32(s.lin1_b, F);
+        L.lin2_w = upload_bf16(s.lin2_w, H * F); L.lin2_b = upload_f32(s.lin2_b, H);
+        m->head.push_back(std::move(L));
+    }
+    m->s_norm_w = upload_f32(w->scorer_norm_w, H);
+    m->s_norm_b = upload_f32(w->scorer_norm_b, H);
+    m->s_w1 = upload_bf16(w->scorer_w1, H * H);
+    m->s_b1 = upload_f32(w->scorer_b1, H);
+    m->s_w2 = upload_f32(w->scorer_w2, H);
+    m->s_b2 = w->scorer_b2;
+    HIP_CHECK(hipDeviceSynchronize());
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* jh_last_error(void) { return jh_error_slot().c_str(); }
+
+void jh_rope_table(float theta, uint32_t head_dim, uint32_t positions, float* cos_out, float* sin_out) {
+    const uint32_t half = head_dim / 2;
+    std::vector<float> inv(half);
+    for (uint32_t i = 0; i < half; ++i) inv[i] = 1.0f / powf(theta, (float)(2 * i) / (float)head_dim);
+    for (uint32_t p = 0; p < positions; ++p)
+        for (uint32_t i = 0; i < half; ++i) {
+            const float f = inv[i] * (float)p;
+            cos_out[(size_t)p * half + i] = cosf(f);
+            sin_out[(size_t)p * half + i] = sinf(f);
+        }
+}
+
+int jh_create(const jh_config* config, const jh_weights* weights, int ordinal, jh_model** out) {
+    return jh_guarded([&] {
+        if (!out) throw jh_error(JH_ERR_INVALID, "null output handle");
+        *out = nullptr;
+        auto m = std::make_unique<jh_model>();
+        build_model(m.get(), config, weights, ordinal);
+        *out = m.release();
+    });
+}
+
+void jh_destroy(jh_model* model) {
+    if (!model) return;
+    (void)hipSetDevice(model->device);
+    if (model->stream) (void)hipStreamSynchronize(model->stream);
+    delete model;
+}
+
+const char* jh_name(jh_model* model) { return model ? model->name.c_str() : ""; }
+
+void* jh_stream(jh_model* model) { return model ? (void*)model->stream : nullptr; }
+
+int jh_set_graph(jh_model* model, int enabled) {
+    return jh_guarded([&] {
+        if (!model) throw jh_error(JH_ERR_INVALID, "null model");
+        std::lock_guard<std::mutex> g(model->mu);
+        model->use_graph = enabled != 0;
+    });
+}
+
+int jh_stage(jh_model* model, const uint32_t* ids, size_t tokens, const uint32_t* starts, const uint32_t* lens,
+             const uint8_t* qtypes, size_t sequences, const uint32_t* marker_rows, size_t markers) {
+    return jh_guarded([&] {
+        if (!model) throw jh_error(JH_ERR_INVALID, "null model");
+        std::lock_guard<std::mutex> g(model->mu);
+        model->bind();
+        model->stage(ids, tokens, starts, lens, qtypes, sequences, marker_rows, markers);
+    });
+}
+
+int jh_execute(jh_model* model) {
+    return jh_guarded([&] {
+        if (!model) throw jh_error(JH_ERR_INVALID, "null model");
+        std::lock_guard<std::mutex> g(model->mu);
+        model->bind();
+        model->execute();
+    });
+}
+
+int jh_scores(jh_model* model, float* scores, size_t markers) {
+    return jh_guarded([&] {
+        if (!model) throw jh_error(JH_ERR_INVALID, "null model");
+        if (markers && !scores) throw jh_error(JH_ERR_INVALID, "null scores buffer");
+        std::lock_guard<std::mutex> g(model->mu);
+        model->bind();
+        model->read_scores(scores, markers);
+    });
+}
+
+int jh_forward(jh_model* model, const uint32_t* ids, size_t tokens, const uint32_t* starts, const uint32_t* lens,
+               const uint8_t* qtypes, size_t sequences, const uint32_t* marker_rows, size_t markers, float* scores) {
+    return jh_guarded([&] {
+        if (!model) throw jh_error(JH_ERR_INVALID, "null model");
+        if (markers && !scores) throw jh_error(JH_ERR_INVALID, "null scores buffer");
+        std::lock_guard<std::mutex> g(model->mu);
+        model->bind();
+        model->stage(ids, tokens, starts, lens, qtypes, sequences, marker_rows, markers);
+        model->execute();
+        model->read_scores(scores, markers);
+    });
+}
+
+int jh_forward_padded(jh_model* model, const uint32_t* ids, size_t batch, size_t padded_len, const uint32_t* lens,
+                      const uint8_t* qtypes, const uint32_t* markers, const uint32_t* marker_starts, float* scores) {
+    return jh_guarded([&] {
+        if (!model) throw jh_error(JH_ERR_INVALID, "null model");
+        if (batch && (!ids || !lens || !qtypes || !marker_starts)) throw jh_error(JH_ERR_INVALID, "null batch array");
+        // Pack away the padding on the host: the device only ever sees real tokens.
+        std::vector<uint32_t> pids, starts(batch), rows;
+        size_t total = 0;
+        for (size_t b = 0; b < batch; ++b) {
+            if (lens[b] > padded_len) throw jh_error(JH_ERR_INVALID, "row length exceeds the padded length");
+            starts[b] = (uint32_t)total;
+            total += lens[b];
+        }
+        pids.reserve(total);
+        for (size_t b = 0; b < batch; ++b) {
+            pids.insert(pids.end(), ids + b * padded_len, ids + b * padded_len + lens[b]);
+            if (marker_starts[b + 1] < marker_starts[b]) throw jh_error(JH_ERR_INVALID, "marker_starts must be non-decreasing");
+            for (uint32_t j = marker_starts[b]; j < marker_starts[b + 1]; ++j) {
+                if (markers[j] >= lens[b]) throw jh_error(JH_ERR_INVALID, "marker outside its row");
+                rows.push_back(starts[b] + markers[j]);
+            }
+        }
+        const size_t m = batch ? marker_starts[batch] : 0;
+        if (m && (!markers || !scores)) throw jh_error(JH_ERR_INVALID, "null marker or score buffer");
+        std::lock_guard<std::mutex> g(model->mu);
+        model->bind();
+        model->stage(pids.data(), total, starts.data(), lens, qtypes, batch, rows.data(), rows.size());
+        model->execute();
+        model->read_scores(scores, m);
+    });
+}
+
+int jh_debug_tokens(jh_model* model, uint32_t* ids_out, uint32_t* pos_out, size_t tokens) {
+    return jh_guarded([&] {
+        if (!model) throw jh_error(JH_ERR_INVALID, "null model");
+        std::lock_guard<std::mutex> g(model->mu);
+        model->bind();
+        if (!model->staged || tokens != model->T) throw jh_error(JH_ERR_INVALID, "token count does not match the staged batch");
+        if (!tokens) return;
+        std::vector<uint32_t> tok(tokens);
+        HIP_CHECK(hipMemcpyAsync(ids_out, model->d_ids, tokens * 4, hipMemcpyDeviceToHost, model->stream));
+        HIP_CHECK(hipMemcpyAsync(tok.data(), model->d_tok, tokens * 4, hipMemcpyDeviceToHost, model->stream));
+        HIP_CHECK(hipStreamSynchronize(model->stream));
+        for (size_t i = 0; i < tokens; ++i) pos_out[i] = tok[i] & 0xffffu;
+    });
+}
+
+int jh_debug_encode(jh_model* model, uint32_t layers, float* x_out, size_t tokens) {
+    return jh_guarded([&] {
+        if (!model) throw jh_error(JH_ERR_INVALID, "null model");
+        std::lock_guard<std::mutex> g(model->mu);
+        model->bind();
+        if (!model->staged || tokens != model->T) throw jh_error(JH_ERR_INVALID, "token count does not match the staged batch");
+        if (layers > (uint32_t)model->nlayers) throw jh_error(JH_ERR_INVALID, "layer count out of range");
+        if (!tokens) return;
+        model->run_encoder((int)layers);
+        HIP_CHECK(hipMemcpyAsync(x_out, model->x.p, tokens * model->h * 4, hipMemcpyDeviceToHost, model->stream));
+        HIP_CHECK(hipStreamSynchronize(model->stream));
+    });
+}
+
+}  // extern "C"

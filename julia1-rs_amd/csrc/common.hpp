@@ -1,0 +1,81 @@
+// Shared device helpers for the gfx950 kernels: bf16 conversion, vector
+// types, wavefront (64-lane) reductions, and the GELU used by the GEGLU and
+// scorer epilogues.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <stdexcept>
+#include <string>
+
+typedef uint16_t bf16_t;  // bf16 bit pattern in memory
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+#define JH_WAVE 64
+
+// Error raised by host code; the C-ABI layer turns it into a return code.
+struct jh_error : std::runtime_error {
+    int code;
+    jh_error(int c, const std::string& m) : std::runtime_error(m), code(c) {}
+};
+
+#define HIP_CHECK(call)                                                                              \
+    do {                                                                                             \
+        hipError_t e_ = (call);                                                                      \
+        if (e_ != hipSuccess)                                                                        \
+            throw jh_error(2, std::string(#call) + ": " + hipGetErrorString(e_));                    \
+    } while (0)
+
+// float -> bf16 bits, round to nearest even, NaN kept quiet (as half::bf16::from_f32).
+__host__ __device__ inline bf16_t f2bf(float f) {
+    uint32_t u = __builtin_bit_cast(uint32_t, f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16_t)((u >> 16) | 0x40);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (bf16_t)(u >> 16);
+}
+
+__host__ __device__ inline float bf2f(bf16_t b) { return __builtin_bit_cast(float, (uint32_t)b << 16); }
+
+// Two floats -> packed bf16x2 (low half = a), RNE.
+__device__ inline uint32_t pack2(float a, float b) { return (uint32_t)f2bf(a) | ((uint32_t)f2bf(b) << 16); }
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, JH_WAVE);
+    return v;
+}
+
+__device__ inline float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, JH_WAVE));
+    return v;
+}
+
+// erf by the rational approximation published in Eigen (ptanh/perf float
+// coefficients, as used by XLA): clamp to [-4, 4], x·P(x²)/Q(x²), |error| < 1e-6.
+__device__ inline float erf_rational(float x) {
+    x = fminf(fmaxf(x, -4.0f), 4.0f);
+    float x2 = x * x;
+    float p = -2.72614225801306e-10f;
+    p = p * x2 + 2.77068142495902e-08f;
+    p = p * x2 + -2.10102402082508e-06f;
+    p = p * x2 + -5.69250639462346e-05f;
+    p = p * x2 + -7.34990630326855e-04f;
+    p = p * x2 + -2.95459980854025e-03f;
+    p = p * x2 + -1.60960333262415e-02f;
+    float q = -1.45660718464996e-05f;
+    q = q * x2 + -2.13374055278905e-04f;
+    q = q * x2 + -1.68282697438203e-03f;
+    q = q * x2 + -7.37332916720468e-03f;
+    q = q * x2 + -1.42647390514189e-02f;
+    return x * p / q;
+}
+
+// Exact-form GELU 0.5·x·(1 + erf(x/√2)), as nn.GELU() / transformers "gelu".
+__device__ inline float gelu_erf(float x) { return 0.5f * x * (1.0f + erf_rational(x * 0.70710678118654752f)); }

@@ -1,0 +1,55 @@
+// Launch wrappers of the gfx950 kernels (implemented in gemm.hip, attention.hip,
+// norm.hip).  Each checks the shapes its kernel assumes and throws jh_error
+// before launching anything that could read or write out of bounds.
+#pragma once
+
+#include "common.hpp"
+
+struct GemmArgs {
+    const bf16_t* x;        // activations, row stride ldx (elements)
+    long ldx;
+    const int32_t* gather;  // optional row indirection for x
+    int rows;
+    const bf16_t* w;        // [n, k] row-major
+    int n, k;
+    void* out;              // row stride ldo (elements), starting at column col
+    long ldo;
+    int col;
+    const float* bias;      // [n] or null
+    const int32_t* pos;     // ROPE: position in the low 16 bits of pos[row]
+    const float* cos_t;     // ROPE: [positions, 32]
+    const float* sin_t;
+    int rope_cols;          // ROPE: columns [0, rope_cols) are rotated
+};
+
+void launch_gemm(int epilogue, const GemmArgs& a, hipStream_t stream);
+
+struct AttnTile {
+    int32_t q_row, nq, kv_row, kv_len, q_pos;
+};
+
+struct AttnArgs {
+    const bf16_t* q;
+    long ldq;
+    const bf16_t* k;
+    const bf16_t* v;
+    long ldkv;
+    bf16_t* out;
+    long ldo;
+    const AttnTile* tiles;
+    int ntiles;
+    int heads;
+    int window;        // < 0: global
+    float scale_log2;  // softmax scale · log2(e)
+};
+
+void launch_attention(const AttnArgs& a, hipStream_t stream);
+
+void launch_embed_ln(const uint32_t* ids, int rows, const float* table, const float* w, float eps, int hidden,
+                     float* x, bf16_t* xn, hipStream_t stream);
+void launch_layer_norm(const float* x, int rows, const float* w, const float* b, float eps, int hidden, bf16_t* out,
+                       hipStream_t stream);
+void launch_final_norm(float* x, int rows, const float* fw, const float* type_emb, const uint32_t* tok_meta,
+                       const float* hw, const float* hb, float eps, int hidden, bf16_t* out, hipStream_t stream);
+void launch_gather_f32(const float* src, const int32_t* idx, int rows, int hidden, float* dst, hipStream_t stream);
+void launch_scorer(const float* z, int rows, int hidden, const float* w2, float b2, float* out, hipStream_t stream);

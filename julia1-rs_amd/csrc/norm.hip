@@ -1,0 +1,237 @@
+// Row kernels for gfx950: one 64-lane wavefront per row, four rows per
+// 256-thread workgroup.  A row of `hidden` floats is held as hidden/64
+// values per lane, loaded with the widest vector that divides them (float4
+// for hidden 768/1024, float2 for 384/128), so every global access is a fully
+// coalesced 64-lane vector load.  LayerNorm is two-pass (mean, then squared
+// deviations) with wavefront-shuffle sums, as in the reference's layer_norm.
+#include <hip/hip_runtime.h>
+
+#include "kernels.hpp"
+
+namespace {
+
+constexpr int ROWS_PER_BLOCK = 4;
+
+template <int EPL>
+struct RowVec {
+    static constexpr int VEC = EPL % 4 == 0 ? 4 : (EPL % 2 == 0 ? 2 : 1);
+    static constexpr int NC = EPL / VEC;  // vector chunks per lane
+    float v[EPL];
+
+    // Chunk c of this lane covers elements [(c*64 + lane)*VEC, +VEC).
+    __device__ static int index(int c, int lane) { return (c * 64 + lane) * VEC; }
+
+    __device__ void load(const float* row, int lane) {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const float* p = row + index(c, lane);
+            if constexpr (VEC == 4) {
+                f32x4 t = *(const f32x4*)p;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[c * 4 + e] = t[e];
+            } else if constexpr (VEC == 2) {
+                float2 t = *(const float2*)p;
+                v[c * 2] = t.x;
+                v[c * 2 + 1] = t.y;
+            } else {
+                v[c] = *p;
+            }
+        }
+    }
+    __device__ void store(float* row, int lane) const {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            float* p = row + index(c, lane);
+            if constexpr (VEC == 4) {
+                *(f32x4*)p = f32x4{v[c * 4], v[c * 4 + 1], v[c * 4 + 2], v[c * 4 + 3]};
+            } else if constexpr (VEC == 2) {
+                *(float2*)p = make_float2(v[c * 2], v[c * 2 + 1]);
+            } else {
+                *p = v[c];
+            }
+        }
+    }
+    __device__ void store_bf16(bf16_t* row, int lane) const {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            bf16_t* p = row + index(c, lane);
+            if constexpr (VEC == 4) {
+                *(u32x2*)p = u32x2{pack2(v[c * 4], v[c * 4 + 1]), pack2(v[c * 4 + 2], v[c * 4 + 3])};
+            } else if constexpr (VEC == 2) {
+                *(uint32_t*)p = pack2(v[c * 2], v[c * 2 + 1]);
+            } else {
+                *p = f2bf(v[c]);
+            }
+        }
+    }
+    // v = (v - mean) * rstd * w (+ b), two-pass statistics over the whole row.
+    __device__ void layer_norm(const float* w, const float* b, float eps, int lane) {
+        constexpr float inv_n = 1.0f / (EPL * 64);
+        float s = 0.0f;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) s += v[e];
+        const float mean = wave_sum(s) * inv_n;
+        float q = 0.0f;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) {
+            float d = v[e] - mean;
+            q += d * d;
+        }
+        const float rstd = 1.0f / __builtin_sqrtf(wave_sum(q) * inv_n + eps);
+        RowVec<EPL> g, bb;
+        g.load(w, lane);
+        if (b) bb.load(b, lane);
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) {
+            float y = (v[e] - mean) * rstd * g.v[e];
+            v[e] = b ? y + bb.v[e] : y;
+        }
+    }
+};
+
+template <int EPL>
+__global__ __launch_bounds__(256) void embed_ln_kernel(const uint32_t* __restrict__ ids, int rows,
+                                                       const float* __restrict__ table, const float* __restrict__ w,
+                                                       float eps, float* __restrict__ x, bf16_t* __restrict__ xn) {
+    constexpr int H = EPL * 64;
+    const int row = blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    RowVec<EPL> r;
+    r.load(table + (long)ids[row] * H, lane);
+    r.layer_norm(w, nullptr, eps, lane);
+    r.store(x + (long)row * H, lane);
+    r.store_bf16(xn + (long)row * H, lane);
+}
+
+template <int EPL>
+__global__ __launch_bounds__(256) void layer_norm_kernel(const float* __restrict__ x, int rows,
+                                                         const float* __restrict__ w, const float* __restrict__ b,
+                                                         float eps, bf16_t* __restrict__ out) {
+    constexpr int H = EPL * 64;
+    const int row = blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    RowVec<EPL> r;
+    r.load(x + (long)row * H, lane);
+    r.layer_norm(w, b, eps, lane);
+    r.store_bf16(out + (long)row * H, lane);
+}
+
+template <int EPL>
+__global__ __launch_bounds__(256) void final_norm_kernel(float* __restrict__ x, int rows, const float* __restrict__ fw,
+                                                         const float* __restrict__ type_emb,
+                                                         const uint32_t* __restrict__ tok_meta,
+                                                         const float* __restrict__ hw, const float* __restrict__ hb,
+                                                         float eps, bf16_t* __restrict__ out) {
+    constexpr int H = EPL * 64;
+    const int row = blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    RowVec<EPL> r, te;
+    float* xr = x + (long)row * H;
+    r.load(xr, lane);
+    r.layer_norm(fw, nullptr, eps, lane);
+    te.load(type_emb + (long)((tok_meta[row] >> 16) & 0xff) * H, lane);
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) r.v[e] += te.v[e];
+    r.store(xr, lane);
+    r.layer_norm(hw, hb, 1e-5f, lane);
+    r.store_bf16(out + (long)row * H, lane);
+}
+
+template <int EPL>
+__global__ __launch_bounds__(256) void gather_kernel(const float* __restrict__ src, const int32_t* __restrict__ idx,
+                                                     int rows, float* __restrict__ dst) {
+    constexpr int H = EPL * 64;
+    const int row = blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    RowVec<EPL> r;
+    r.load(src + (long)idx[row] * H, lane);
+    r.store(dst + (long)row * H, lane);
+}
+
+template <int EPL>
+__global__ __launch_bounds__(256) void scorer_kernel(const float* __restrict__ z, int rows, const float* __restrict__ w2,
+                                                     float b2, float* __restrict__ out) {
+    constexpr int H = EPL * 64;
+    const int row = blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    RowVec<EPL> r, w;
+    r.load(z + (long)row * H, lane);
+    w.load(w2, lane);
+    float s = 0.0f;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) s += gelu_erf(r.v[e]) * w.v[e];
+    s = wave_sum(s);
+    if (lane == 0) out[row] = s + b2;
+}
+
+// Calls f.template operator()<EPL>() for hidden = 64*EPL in the supported set.
+template <class F>
+void dispatch_hidden(int hidden, F&& f) {
+    switch (hidden) {
+        case 64: f.template operator()<1>(); break;
+        case 128: f.template operator()<2>(); break;
+        case 192: f.template operator()<3>(); break;
+        case 256: f.template operator()<4>(); break;
+        case 320: f.template operator()<5>(); break;
+        case 384: f.template operator()<6>(); break;
+        case 448: f.template operator()<7>(); break;
+        case 512: f.template operator()<8>(); break;
+        case 576: f.template operator()<9>(); break;
+        case 640: f.template operator()<10>(); break;
+        case 704: f.template operator()<11>(); break;
+        case 768: f.template operator()<12>(); break;
+        case 832: f.template operator()<13>(); break;
+        case 896: f.template operator()<14>(); break;
+        case 960: f.template operator()<15>(); break;
+        case 1024: f.template operator()<16>(); break;
+        default: throw jh_error(1, "row kernels support hidden = 64*k for k in 1..16");
+    }
+}
+
+inline dim3 row_grid(int rows) { return dim3((rows + ROWS_PER_BLOCK - 1) / ROWS_PER_BLOCK); }
+
+}  // namespace
+
+void launch_embed_ln(const uint32_t* ids, int rows, const float* table, const float* w, float eps, int hidden,
+                     float* x, bf16_t* xn, hipStream_t s) {
+    if (rows <= 0) return;
+    dispatch_hidden(hidden, [&]<int EPL>() {
+        hipLaunchKernelGGL(embed_ln_kernel<EPL>, row_grid(rows), dim3(256), 0, s, ids, rows, table, w, eps, x, xn);
+    });
+    HIP_CHECK(hipGetLastError());
+}
+
+void launch_layer_norm(const float* x, int rows, const float* w, const float* b, float eps, int hidden, bf16_t* out,
+                       hipStream_t s) {
+    if (rows <= 0) return;
+    dispatch_hidden(hidden, [&]<int EPL>() {
+        hipLaunchKernelGGL(layer_norm_kernel<EPL>, row_grid(rows), dim3(256), 0, s, x, rows, w, b, eps, out);
+    });
+    HIP_CHECK(hipGetLastError());
+}
+
+void launch_final_norm(float* x, int rows, const float* fw, const float* type_emb, const uint32_t* tok_meta,
+                       const float* hw, const float* hb, float eps, int hidden, bf16_t* out, hipStream_t s) {
+    if (rows <= 0) return;
+    dispatch_hidden(hidden, [&]<int EPL>() {
+        hipLaunchKernelGGL(final_norm_kernel<EPL>, row_grid(rows), dim3(256), 0, s, x, rows, fw, type_emb, tok_meta,
+                           hw, hb, eps, out);
+    });
+    HIP_CHECK(hipGetLastError());
+}
+
+void launch_gather_f32(const float* src, const int32_t* idx, int rows, int hidden, float* dst, hipStream_t s) {
+    if (rows <= 0) return;
+    dispatch_hidden(hidden, [&]<int EPL>() {
+        hipLaunchKernelGGL(gather_kernel<EPL>, row_grid(rows), dim3(256), 0, s, src, idx, rows, dst);
+    });
+    HIP_CHECK(hipGetLastError());
+}
+
+void launch_scorer(const float* z, int rows, int hidden, const float* w2, float b2, float* out, hipStream_t s) {
+    if (rows <= 0) return;
+    dispatch_hidden(hidden, [&]<int EPL>() {
+        hipLaunchKernelGGL(scorer_kernel<EPL>, row_grid(rows), dim3(256), 0, s, z, rows, w2, b2, out);
+    });
+    HIP_CHECK(hipGetLastError());
+}

@@ -1,0 +1,148 @@
+"""Full encoder-forward parity on the GPU (jh_forward through the C-ABI)
+against the FP32 CPU oracle on identical synthetic weights and batches.
+
+Gates: |Δlogit| <= 2e-2, |Δsoftmax| <= 1e-2 (f64
+softmax per row, as answers_from_logits, src/typed.rs:115-131), argmax
+agreement >= 99.9% (first-max rule, src/request.rs:164-172), token ids and
+positions bit-exact.
+"""
+import numpy as np
+import pytest
+
+from julia1_amd import abi, hip, synth
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def softmax64(z):
+    z = np.asarray(z, dtype=np.float64)
+    e = np.exp(z - z.max())
+    return e / e.sum()
+
+
+def parity(batch, got, ref):
+    """Per-row logit / softmax / argmax comparison; returns a summary dict."""
+    g, r = batch.split_scores(got), batch.split_scores(ref)
+    dl = max((np.abs(a - b).max() for a, b in zip(g, r) if a.size), default=0.0)
+    dp = max((np.abs(softmax64(a) - softmax64(b)).max() for a, b in zip(g, r) if a.size), default=0.0)
+    agree = sum(int(np.argmax(a) == np.argmax(b)) for a, b in zip(g, r) if a.size)
+    rows = sum(1 for a in g if a.size)
+    gaps = [np.sort(b)[-1] - np.sort(b)[-2] for b in r if b.size > 1]
+    return dict(max_dlogit=float(dl), max_dsoftmax=float(dp), argmax_agree=agree, rows=rows,
+                min_gap=float(min(gaps)) if gaps else None)
+
+
+def check_gates(s):
+    assert s["max_dlogit"] <= 2e-2, s
+    assert s["max_dsoftmax"] <= 1e-2, s
+    assert s["argmax_agree"] >= 0.999 * s["rows"] or s["argmax_agree"] == s["rows"], s
+
+
+@pytest.fixture(scope="module")
+def tiny():
+    cfg = synth.model_config("tiny")
+    ws = abi.WeightSet(cfg, synth.make_weights(cfg, seed=11))
+    return ws, hip.HipModel(ws), oracle.OracleModel(ws)
+
+
+@pytest.fixture(scope="module")
+def base():
+    cfg = synth.model_config("modernbert-base")
+    ws = abi.WeightSet(cfg, synth.make_weights(cfg, seed=0))
+    return ws, hip.HipModel(ws), oracle.OracleModel(ws)
+
+
+def test_name(tiny):
+    assert tiny[1].name.startswith("hip:0 (")
+
+
+def test_tiny_tokens_and_positions_bit_exact(tiny):
+    ws, gpu, _ = tiny
+    b = synth.make_batch([40, 1, 17, 130], [3, 1, 2, 5], ws.cfg.vocab, 5)
+    gpu.stage(b)
+    ids, pos = gpu.debug_tokens(b.tokens)
+    assert np.array_equal(ids, b.ids)
+    assert np.array_equal(pos, np.concatenate([np.arange(n) for n in b.lens]).astype(np.uint32))
+
+
+def test_tiny_layerwise(tiny):
+    ws, gpu, orc = tiny
+    b = synth.make_batch([40, 1, 17, 130], [3, 1, 2, 5], ws.cfg.vocab, 5)
+    gpu.stage(b)
+    for layers in range(ws.cfg.layers + 1):
+        x = gpu.debug_encode(b.tokens, layers)
+        xr = orc.encode(b, layers)
+        assert np.abs(x - xr).max() < 3e-2 * (layers + 1), (layers, np.abs(x - xr).max())
+
+
+def test_tiny_forward(tiny):
+    ws, gpu, orc = tiny
+    b = synth.make_batch([40, 1, 17, 130, 64, 65], [3, 1, 2, 5, 20, 7], ws.cfg.vocab, 6)
+    s = parity(b, gpu.forward(b), orc.forward(b))
+    check_gates(s)
+
+
+def test_base_config0(base):
+    ws, gpu, orc = base
+    b = synth.workload("config0")
+    s = parity(b, gpu.forward(b), orc.forward(b))
+    print("config0", s)
+    check_gates(s)
+
+
+def test_base_config1(base):
+    ws, gpu, orc = base
+    b = synth.workload("config1")
+    got = gpu.forward(b)
+    s = parity(b, got, orc.forward(b))
+    print("config1", s)
+    check_gates(s)
+
+
+def test_padded_equals_packed(base):
+    ws, gpu, _ = base
+    b = synth.workload("config1").subset(range(8))
+    ids, lens, qt, markers, mst = synth.padded(b, 512)
+    assert np.array_equal(gpu.forward_padded(ids, lens, qt, markers, mst), gpu.forward(b))
+
+
+def test_batching_invariance(base):
+    """A row's logits do not depend on what else is in the batch (src tests/checkpoint.rs:91-105)."""
+    ws, gpu, _ = base
+    b = synth.workload("config1").subset(range(6))
+    together = b.split_scores(gpu.forward(b))
+    for i in range(6):
+        alone = gpu.forward(b.subset([i]))
+        assert np.abs(alone - together[i]).max() <= 1e-4
+
+
+def test_graph_replay_matches_eager(base):
+    ws, gpu, _ = base
+    b = synth.workload("config1").subset(range(10))
+    gpu.set_graph(False)
+    eager = gpu.forward(b)
+    gpu.set_graph(True)
+    gpu.stage(b)
+    for _ in range(3):
+        gpu.execute()
+        assert np.array_equal(gpu.scores(b.marker_rows.size), eager)
+    gpu.set_graph(True)
+
+
+def test_invalid_batches_rejected(tiny):
+    ws, gpu, _ = tiny
+    b = synth.make_batch([10, 5], [2, 1], ws.cfg.vocab, 1)
+    bad = abi.Batch(b.ids.copy(), b.starts, b.lens, b.qtypes, b.marker_rows, b.marker_starts)
+    bad.ids[3] = ws.cfg.vocab
+    with pytest.raises(hip.HipError):
+        gpu.forward(bad)
+    bad = abi.Batch(b.ids, b.starts, b.lens, b.qtypes, np.array([12, 3], dtype=np.uint32), b.marker_starts)
+    with pytest.raises(hip.HipError):
+        gpu.forward(bad)
+    long = synth.make_batch([ws.cfg.max_positions + 1], [1], ws.cfg.vocab, 1)
+    with pytest.raises(hip.HipError):
+        gpu.forward(long)
+    # the model still works after rejected calls
+    s = parity(b, gpu.forward(b), tiny[2].forward(b))
+    check_gates(s)

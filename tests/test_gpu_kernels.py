@@ -1,0 +1,275 @@
+"""Kernel-level parity on the GPU: every gfx950 kernel through the C-ABI
+(include/julia1_hip_ops.h) against an f64 reference of the same bf16/f32
+inputs, and against the FP32 oracle where the oracle has the same op.
+
+Tolerances: bf16 outputs carry one RNE rounding (relative 2^-9), so they are
+held to 4e-3 relative; FP32 outputs to 1e-4 of the operand scale (FP32
+accumulation-order differences only).
+"""
+import math
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+from julia1_amd import abi, hip  # noqa: E402
+from oracle import oracle  # noqa: E402
+from gpu_util import bf16_round, dev, host  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+BF16 = torch.bfloat16
+
+
+def rng(seed):
+    return np.random.default_rng(seed)
+
+
+def _gemm_inputs(r, rows, n, k):
+    x = bf16_round(r.standard_normal((rows, k), dtype=np.float32))
+    w = bf16_round(r.standard_normal((n, k), dtype=np.float32) * 0.02)
+    return x, w, x.astype(np.float64) @ w.astype(np.float64).T
+
+
+SHAPES = [(1, 64, 64), (37, 128, 768), (130, 384, 1152), (257, 2304, 768), (64, 768, 3072)]
+
+
+@pytest.mark.parametrize("rows,n,k", SHAPES)
+def test_gemm_store_bf16(rows, n, k):
+    x, w, ref = _gemm_inputs(rng(1), rows, n, k)
+    out = torch.zeros(rows, n + 8, dtype=BF16, device="cuda")
+    hip.op_gemm(abi.EPI_STORE_BF16, dev(x, BF16), dev(w, BF16), out, col=4)
+    got = host(out)
+    assert np.all(got[:, :4] == 0) and np.all(got[:, 4 + n:] == 0)
+    d = np.abs(got[:, 4:4 + n] - ref)
+    assert np.all(d <= 4e-3 * np.abs(ref) + 1e-6), d.max()
+
+
+@pytest.mark.parametrize("rows,n,k", SHAPES)
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_gemm_resid_f32(rows, n, k, with_bias):
+    r = rng(2)
+    x, w, ref = _gemm_inputs(r, rows, n, k)
+    base = r.standard_normal((rows, n), dtype=np.float32)
+    bias = r.standard_normal(n, dtype=np.float32) if with_bias else None
+    out = dev(base)
+    hip.op_gemm(abi.EPI_RESID_F32, dev(x, BF16), dev(w, BF16), out, bias=None if bias is None else dev(bias))
+    expect = base + ref + (0 if bias is None else bias)
+    assert np.abs(host(out) - expect).max() < 1e-4 * math.sqrt(k) * 0.02 * 4 + 1e-5
+
+
+@pytest.mark.parametrize("epi", [abi.EPI_BIAS_BF16, abi.EPI_BIAS_RELU_BF16, abi.EPI_BIAS_F32])
+def test_gemm_bias_epilogues(epi):
+    r = rng(3)
+    rows, n, k = 200, 384, 768
+    x, w, ref = _gemm_inputs(r, rows, n, k)
+    bias = r.standard_normal(n, dtype=np.float32) * 0.1
+    dt = torch.float32 if epi == abi.EPI_BIAS_F32 else BF16
+    out = torch.zeros(rows, n, dtype=dt, device="cuda")
+    hip.op_gemm(epi, dev(x, BF16), dev(w, BF16), out, bias=dev(bias))
+    expect = ref + bias
+    if epi == abi.EPI_BIAS_RELU_BF16:
+        expect = np.maximum(expect, 0)
+    tol = 1e-5 if epi == abi.EPI_BIAS_F32 else 4e-3 * np.abs(expect) + 1e-6
+    assert np.all(np.abs(host(out) - expect) <= tol)
+
+
+def test_gemm_gather_rows():
+    r = rng(4)
+    x, w, ref = _gemm_inputs(r, 300, 256, 512)
+    idx = np.array([5, 0, 299, 17, 17, 100, 3], dtype=np.int32)
+    out = torch.zeros(idx.size, 256, dtype=torch.float32, device="cuda")
+    bias = np.zeros(256, dtype=np.float32)
+    hip.op_gemm(abi.EPI_BIAS_F32, dev(x, BF16), dev(w, BF16), out, rows=idx.size, gather=dev(idx), bias=dev(bias))
+    assert np.abs(host(out) - ref[idx]).max() < 1e-5
+
+
+@pytest.mark.parametrize("rows,inter,k", [(1, 64, 128), (77, 192, 128), (300, 1152, 768)])
+def test_gemm_geglu(rows, inter, k):
+    r = rng(5)
+    x = bf16_round(r.standard_normal((rows, k), dtype=np.float32))
+    wi = bf16_round(r.standard_normal((2 * inter, k), dtype=np.float32) * 0.05)
+    prod = x.astype(np.float64) @ wi.astype(np.float64).T
+    u, v = prod[:, :inter], prod[:, inter:]
+    erf = np.vectorize(math.erf)
+    expect = 0.5 * u * (1 + erf(u / math.sqrt(2))) * v
+    out = torch.zeros(rows, inter, dtype=BF16, device="cuda")
+    hip.op_gemm(abi.EPI_GEGLU_BF16, dev(x, BF16), dev(hip.interleave_geglu(wi), BF16), out)
+    d = np.abs(host(out) - expect)
+    assert np.all(d <= 4e-3 * np.abs(expect) + 2e-6), d.max()
+    # and the oracle's fused GEGLU on the same values
+    assert np.all(np.abs(oracle.linear_geglu(x, wi) - expect) <= 1e-5 * (1 + np.abs(expect)))
+
+
+@pytest.mark.parametrize("theta", [10000.0, 160000.0])
+def test_gemm_rope(theta):
+    r = rng(6)
+    rows, h, k = 150, 256, 256
+    n = 3 * h
+    x, w, ref = _gemm_inputs(r, rows, n, k)
+    pos = r.integers(0, 8192, rows).astype(np.int32)
+    cos, sin = oracle.rope_table(theta, 8192)
+    expect = ref.copy()
+    for hd in range(0, 2 * h, 64):
+        a, b = ref[:, hd:hd + 32], ref[:, hd + 32:hd + 64]
+        c, s = cos[pos].astype(np.float64), sin[pos].astype(np.float64)
+        expect[:, hd:hd + 32] = a * c - b * s
+        expect[:, hd + 32:hd + 64] = b * c + a * s
+    scale = np.abs(ref).copy()
+    for hd in range(0, 2 * h, 64):
+        m = np.abs(ref[:, hd:hd + 32]) + np.abs(ref[:, hd + 32:hd + 64])
+        scale[:, hd:hd + 32] = m
+        scale[:, hd + 32:hd + 64] = m
+    out = torch.zeros(rows, n, dtype=BF16, device="cuda")
+    hip.op_gemm(abi.EPI_ROPE_BF16, dev(x, BF16), dev(w, BF16), out, pos=dev(pos), cos=dev(cos), sin=dev(sin),
+                rope_cols=2 * h)
+    d = np.abs(host(out) - expect)
+    assert np.all(d <= 4e-3 * scale + 1e-6), d.max()
+
+
+def test_gemm_rejects_bad_shapes():
+    x = torch.zeros(4, 100, dtype=BF16, device="cuda")
+    w = torch.zeros(64, 100, dtype=BF16, device="cuda")
+    out = torch.zeros(4, 64, dtype=BF16, device="cuda")
+    with pytest.raises(hip.HipError):
+        hip.op_gemm(abi.EPI_STORE_BF16, x, w, out)
+
+
+@pytest.mark.parametrize("hidden", [128, 384, 768])
+def test_embed_and_layer_norm(hidden):
+    r = rng(7)
+    vocab, rows = 1000, 333
+    table = r.standard_normal((vocab, hidden), dtype=np.float32) * 0.02
+    w = 1 + 0.1 * r.standard_normal(hidden, dtype=np.float32)
+    b = 0.1 * r.standard_normal(hidden, dtype=np.float32)
+    ids = r.integers(0, vocab, rows).astype(np.uint32)
+    x = torch.zeros(rows, hidden, device="cuda")
+    xn = torch.zeros(rows, hidden, dtype=BF16, device="cuda")
+    hip.op_embed_ln(dev(ids.astype(np.int32)), dev(table), dev(w), 1e-5, x, xn)
+    expect = oracle.layer_norm(table[ids], w, None, 1e-5)
+    assert np.abs(host(x) - expect).max() < 2e-5
+    assert np.all(np.abs(host(xn) - expect) <= 4e-3 * np.abs(expect) + 1e-6)
+    # f64 closed form
+    t = table[ids].astype(np.float64)
+    ln = (t - t.mean(1, keepdims=True)) / np.sqrt(t.var(1, keepdims=True) + 1e-5) * w
+    assert np.abs(host(x) - ln).max() < 2e-5
+    out = torch.zeros(rows, hidden, dtype=BF16, device="cuda")
+    xs = r.standard_normal((rows, hidden), dtype=np.float32) * 3 + 1
+    hip.op_layer_norm(dev(xs), dev(w), dev(b), 1e-5, out)
+    expect = oracle.layer_norm(xs, w, b, 1e-5)
+    assert np.all(np.abs(host(out) - expect) <= 4e-3 * np.abs(expect) + 1e-5)
+
+
+def test_final_norm_and_scorer():
+    r = rng(8)
+    rows, hidden = 97, 768
+    x0 = r.standard_normal((rows, hidden), dtype=np.float32)
+    fw = 1 + 0.1 * r.standard_normal(hidden, dtype=np.float32)
+    te = 0.02 * r.standard_normal((3, hidden), dtype=np.float32)
+    hw = 1 + 0.1 * r.standard_normal(hidden, dtype=np.float32)
+    hb = 0.1 * r.standard_normal(hidden, dtype=np.float32)
+    qt = r.integers(0, 3, rows)
+    pos = r.integers(0, 8192, rows)
+    meta = (pos | (qt << 16)).astype(np.uint32)
+    x = dev(x0)
+    out = torch.zeros(rows, hidden, dtype=BF16, device="cuda")
+    hip.op_final_norm(x, dev(fw), dev(te), dev(meta.astype(np.int32)), dev(hw), dev(hb), 1e-5, out)
+    x1 = oracle.layer_norm(x0, fw, None, 1e-5) + te[qt]
+    assert np.abs(host(x) - x1).max() < 2e-5
+    e2 = oracle.layer_norm(x1, hw, hb, 1e-5)
+    assert np.all(np.abs(host(out) - e2) <= 4e-3 * np.abs(e2) + 1e-5)
+    # gather + scorer
+    idx = np.array([3, 1, 96, 50], dtype=np.int32)
+    dst = torch.zeros(idx.size, hidden, device="cuda")
+    hip.op_gather_f32(x, dev(idx), dst)
+    assert np.array_equal(host(dst), host(x)[idx])
+    z = r.standard_normal((rows, hidden), dtype=np.float32)
+    w2 = 0.02 * r.standard_normal(hidden, dtype=np.float32)
+    s = torch.zeros(rows, device="cuda")
+    hip.op_scorer(dev(z), dev(w2), 0.25, s)
+    erf = np.vectorize(math.erf)
+    z64 = z.astype(np.float64)
+    expect = (0.5 * z64 * (1 + erf(z64 / math.sqrt(2))) * w2).sum(1) + 0.25
+    assert np.abs(host(s) - expect).max() < 1e-4
+
+
+def _attn_ref64(q, k, v, seqs, heads, window, scale=0.125):
+    """f64 softmax(scale·QKᵀ + mask)·V per (sequence, head); seqs = (q_row, nq, kv_row, len, q_pos)."""
+    out = np.zeros((q.shape[0], heads * 64))
+    for q_row, nq, kv_row, ln, q_pos in seqs:
+        for hh in range(heads):
+            Q = q[q_row:q_row + nq, hh * 64:(hh + 1) * 64].astype(np.float64)
+            K = k[kv_row:kv_row + ln, hh * 64:(hh + 1) * 64].astype(np.float64)
+            V = v[kv_row:kv_row + ln, hh * 64:(hh + 1) * 64].astype(np.float64)
+            s = scale * Q @ K.T
+            if window >= 0:
+                qp = q_pos + np.arange(nq)[:, None]
+                kp = np.arange(ln)[None, :]
+                s = np.where(np.abs(qp - kp) <= window, s, -np.inf)
+            s = s - s.max(1, keepdims=True)
+            p = np.exp(s)
+            p /= p.sum(1, keepdims=True)
+            out[q_row:q_row + nq, hh * 64:(hh + 1) * 64] = p @ V
+    return out
+
+
+def _tiles(lens, qt=64):
+    tiles, start = [], 0
+    for ln in lens:
+        for q0 in range(0, ln, qt):
+            tiles.append((start + q0, min(qt, ln - q0), start, ln, q0))
+        start += ln
+    return tiles
+
+
+@pytest.mark.parametrize("window", [-1, 64, 8, 0])
+def test_attention_varlen(window):
+    r = rng(9)
+    heads = 3
+    h = heads * 64
+    lens = [1, 5, 63, 64, 65, 200, 300]
+    t = sum(lens)
+    qkv = bf16_round(r.standard_normal((t, 3 * h), dtype=np.float32))
+    q, k, v = qkv[:, :h], qkv[:, h:2 * h], qkv[:, 2 * h:]
+    tiles = _tiles(lens)
+    seqs = []
+    start = 0
+    for ln in lens:
+        seqs.append((start, ln, start, ln, 0))
+        start += ln
+    expect = _attn_ref64(q, k, v, seqs, heads, window)
+    dq = dev(qkv, BF16)
+    out = torch.zeros(t, h, dtype=BF16, device="cuda")
+    hip.op_attention(dq, 3 * h, dq[:, h:], dq[:, 2 * h:], 3 * h, out, h, dev(np.array(tiles, dtype=np.int32)), heads,
+                     window)
+    got = host(out)
+    assert np.abs(got - expect).max() < 2e-2, np.abs(got - expect).max()
+    # the oracle's attention on the same values, same window semantics
+    orc = oracle.attention(qkv, qkv, [(s[0], s[1], s[2], s[3]) for s in seqs], heads, window)
+    assert np.abs(orc - expect).max() < 1e-4
+
+
+def test_attention_marker_queries():
+    """Queries from a separate buffer (the marker-only head layer) against full keys."""
+    r = rng(10)
+    heads, h = 2, 128
+    lens = [40, 130, 7]
+    t = sum(lens)
+    kv = bf16_round(r.standard_normal((t, 3 * h), dtype=np.float32))
+    markers = [[1, 5, 39], list(range(0, 130, 2)), [0, 6]]
+    nm = sum(len(m) for m in markers)
+    qm = bf16_round(r.standard_normal((nm, h), dtype=np.float32))
+    tiles, seqs, start, mi = [], [], 0, 0
+    for ln, ms in zip(lens, markers):
+        for j in range(0, len(ms), 64):
+            tiles.append((mi + j, min(64, len(ms) - j), start, ln, 0))
+        seqs.append((mi, len(ms), start, ln, 0))
+        start += ln
+        mi += len(ms)
+    expect = _attn_ref64(qm, kv[:, h:2 * h], kv[:, 2 * h:], seqs, heads, -1)
+    dkv = dev(kv, BF16)
+    out = torch.zeros(nm, h, dtype=BF16, device="cuda")
+    hip.op_attention(dev(qm, BF16), h, dkv[:, h:], dkv[:, 2 * h:], 3 * h, out, h,
+                     dev(np.array(tiles, dtype=np.int32)), heads, -1)
+    assert np.abs(host(out) - expect).max() < 2e-2
