@@ -1,0 +1,248 @@
+"""Encoder-forward benchmark on one MI355X (gfx950).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload config1] [--no-cpu] [--no-extra]
+
+A step is one full forward of the HIP backend (embedding + 22 ModernBERT
+layers + decision head + scorer, token ids -> option logits) over one
+synthetic batch that is already resident in HBM (jh_stage before timing;
+jh_execute per step).  Workload config1: 32 rows,
+lengths U[64,512] from a seed, 2-20 options per row, packed without padding.
+Weights are random-init N(0, 0.02) of the ModernBERT-base shape.
+
+Prints ONE JSON line.  `value` is real (unpadded) tokens per second.  The
+`roofline` object is for the kernel class with the largest device time:
+achieved = its algorithmic FLOPs (2·M·N·K) per launch / its mean launch time,
+measured with HIP events on the model's stream over K profiled steps.
+`cpu_baseline` times the FP32 CPU oracle (C++ restatement of the reference's
+src/cpu path) on this host's cores, on the same batch.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "julia1-rs_amd"))
+sys.path.insert(0, ROOT)
+
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+METRIC = "encoder tokens/sec @B=32,L=512 BF16; GEMM MFMA util %; attn ms @L=8192"
+ENCODER_GEMMS = ("gemm_qkv_rope", "gemm_wo_resid", "gemm_wi_geglu", "gemm_wo2_resid")
+MFMA_CLASSES = ENCODER_GEMMS + ("attn_global", "attn_local", "head_gemm", "head_attn")
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def roofline(stat):
+    per_launch_ms = stat["ms"] / stat["launches"]
+    if stat["name"] in MFMA_CLASSES:
+        achieved = stat["flops"] / stat["launches"] / (per_launch_ms * 1e-3) / 1e12
+        return dict(bound="mfma", achieved=round(achieved, 2), peak=PEAK_BF16_TFLOPS, unit="TFLOP/s",
+                    frac=round(achieved / PEAK_BF16_TFLOPS, 4), traffic=None,
+                    kernel=stat["name"], launch_us=round(per_launch_ms * 1e3, 2),
+                    flops_per_launch=stat["flops"] / stat["launches"])
+    achieved = stat["bytes"] / stat["launches"] / (per_launch_ms * 1e-3) / 1e9
+    return dict(bound="hbm", achieved=round(achieved, 1), peak=PEAK_HBM_GBS, unit="GB/s",
+                frac=round(achieved / PEAK_HBM_GBS, 4), traffic=None, kernel=stat["name"],
+                launch_us=round(per_launch_ms * 1e3, 2), bytes_per_launch=stat["bytes"] / stat["launches"])
+
+
+def kernel_table(stats, steps):
+    out = []
+    for s in sorted(stats, key=lambda s: -s["ms"]):
+        mfma = s["name"] in MFMA_CLASSES
+        t = s["ms"] * 1e-3
+        out.append(dict(name=s["name"], ms_per_step=round(s["ms"] / steps, 4), launches_per_step=s["launches"] // steps,
+                        tflops=round(s["flops"] / t / 1e12, 1) if s["flops"] else None,
+                        gbs=round(s["bytes"] / t / 1e9, 1),
+                        frac=round((s["flops"] / t / 1e12 / PEAK_BF16_TFLOPS) if mfma else
+                                   (s["bytes"] / t / 1e9 / PEAK_HBM_GBS), 4)))
+    return out
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="config1", choices=["config0", "config1", "config3", "config4"])
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
+    ap.add_argument("--no-extra", action="store_true", help="skip the GEMM sweep and the L=8192 attention run")
+    ap.add_argument("--cpu-threads", type=int, default=None)
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this build runs on one GPU only: the encoder forward has no cross-sequence "
+                                   "exchange and shards by rows with no collective; run with --gpus 1",
+                          "n_gpus": args.gpus, "skipped": True}))
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+    from julia1_amd import abi, hip, synth
+
+    t0 = time.time()
+    cfg = synth.model_config("modernbert-base")
+    tensors = synth.make_weights(cfg, seed=0)
+    ws = abi.WeightSet(cfg, tensors)
+    model = hip.HipModel(ws)
+    log(f"model ready on {model.name} in {time.time() - t0:.1f}s")
+    batch = synth.workload(args.workload)
+    tokens, markers = batch.tokens, batch.marker_rows.size
+
+    # ---- timed region: K forwards of the staged batch (graph replay), bracketed by syncs
+    model.stage(batch)
+    for _ in range(args.warmup):
+        model.execute()
+    gpu_scores = model.scores(markers)
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    for _ in range(args.steps):
+        model.execute()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t_start
+    ms_per_step = elapsed / args.steps * 1e3
+    value = tokens * args.steps / elapsed
+    log(f"{args.workload}: {tokens} tokens, {ms_per_step:.3f} ms/step, {value:,.0f} tokens/s")
+
+    # PCIe-inclusive rate (host batch in, scores out) for reference: jh_forward per step.
+    t1 = time.perf_counter()
+    for _ in range(max(3, args.steps // 4)):
+        model.forward(batch)
+    fwd_ms = (time.perf_counter() - t1) / max(3, args.steps // 4) * 1e3
+
+    # ---- per-kernel device time: the same K steps, eager with HIP events per launch
+    model.profile(True)
+    for _ in range(args.steps):
+        model.execute()
+    stats = model.profile_read()
+    model.profile(False)
+    kern = kernel_table(stats, args.steps)
+    dominant = max(stats, key=lambda s: s["ms"])
+    roof = roofline(dominant)
+    gemm_ms = sum(s["ms"] for s in stats if s["name"] in ENCODER_GEMMS)
+    gemm_flops = sum(s["flops"] for s in stats if s["name"] in ENCODER_GEMMS)
+    gemm_util = gemm_flops / (gemm_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS * 100
+    prof_step_ms = sum(s["ms"] for s in stats) / args.steps
+
+    extra = {}
+    if not args.no_extra:
+        # Long context: 4 x 8192, every 3rd layer global.
+        b3 = synth.workload("config3")
+        model.stage(b3)
+        model.execute()
+        model.scores(b3.marker_rows.size)
+        model.profile(True)
+        reps = 3
+        for _ in range(reps):
+            model.execute()
+        s3 = model.profile_read()
+        model.profile(False)
+        attn = [s for s in s3 if s["name"] in ("attn_global", "attn_local")]
+        attn_ms = sum(s["ms"] for s in attn) / reps
+        attn_flops = sum(s["flops"] for s in attn) / reps
+        model.stage(b3)
+        model.execute()
+        torch.cuda.synchronize()
+        t3 = time.perf_counter()
+        for _ in range(reps):
+            model.execute()
+        torch.cuda.synchronize()
+        f3 = (time.perf_counter() - t3) / reps * 1e3
+        extra["long_context"] = dict(
+            workload="config3: 4 x 8192 tokens", forward_ms=round(f3, 3), tokens_per_s=round(b3.tokens / f3 * 1e3),
+            encoder_attn_ms=round(attn_ms, 3), encoder_attn_ms_per_sequence=round(attn_ms / 4, 3),
+            attn_tflops=round(attn_flops / (attn_ms * 1e-3) / 1e12, 1),
+            attn_mfma_frac=round(attn_flops / (attn_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+            kernels=kernel_table(s3, reps))
+        log(f"config3: forward {f3:.2f} ms, encoder attention {attn_ms:.2f} ms")
+        # Isolated GEMM sweep: M = 16384.
+        M = 16384
+        g = torch.Generator(device="cpu").manual_seed(2)
+        A = torch.randn(M, 1152, generator=g).bfloat16().cuda()
+        sweep = []
+        stream = torch.cuda.current_stream()
+        for name, epi, n, k in (("wqkv", abi.EPI_STORE_BF16, 2304, 768), ("attn_out_resid", abi.EPI_RESID_F32, 768, 768),
+                                ("wi_geglu", abi.EPI_GEGLU_BF16, 2304, 768),
+                                ("mlp_out_resid", abi.EPI_RESID_F32, 768, 1152)):
+            W = (torch.randn(n, k, generator=g) * 0.02).bfloat16().cuda()
+            X = A[:, :k].contiguous()
+            if epi == abi.EPI_RESID_F32:
+                out = torch.zeros(M, n, device="cuda")
+            elif epi == abi.EPI_GEGLU_BF16:
+                out = torch.zeros(M, n // 2, dtype=torch.bfloat16, device="cuda")
+            else:
+                out = torch.zeros(M, n, dtype=torch.bfloat16, device="cuda")
+            for _ in range(3):
+                hip.op_gemm(epi, X, W, out, stream=stream.cuda_stream)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            reps = 20
+            e0.record(stream)
+            for _ in range(reps):
+                hip.op_gemm(epi, X, W, out, stream=stream.cuda_stream)
+            e1.record(stream)
+            e1.synchronize()
+            ms = e0.elapsed_time(e1) / reps
+            fl = 2.0 * M * n * k
+            byts = M * k * 2 + n * k * 2 + (M * n * 8 if epi == abi.EPI_RESID_F32 else
+                                           M * n // 2 * 2 if epi == abi.EPI_GEGLU_BF16 else M * n * 2)
+            tf = fl / (ms * 1e-3) / 1e12
+            sweep.append(dict(gemm=name, M=M, N=n, K=k, us=round(ms * 1e3, 2), tflops=round(tf, 1),
+                              mfma_frac=round(tf / PEAK_BF16_TFLOPS, 4),
+                              roofline_frac=round(max(fl / (PEAK_BF16_TFLOPS * 1e12), byts / (PEAK_HBM_GBS * 1e9))
+                                                  / (ms * 1e-3), 4)))
+        extra["gemm_sweep"] = sweep
+        log("sweep:", sweep)
+
+    cpu = None
+    parity = None
+    if not args.no_cpu:
+        from oracle import oracle
+        threads = args.cpu_threads or min(16, len(os.sched_getaffinity(0)))
+        orc = oracle.OracleModel(ws, threads=threads)
+        orc.forward(batch.subset([0]))
+        times = []
+        ref = None
+        for _ in range(3):
+            tc = time.perf_counter()
+            ref = orc.forward(batch)
+            times.append(time.perf_counter() - tc)
+        med = statistics.median(times)
+        cpu = dict(value=round(tokens / med, 1), unit="tokens/s", cores=threads, kind="port",
+                   sample=f"{args.workload}: full batch ({tokens} tokens), median of 3 forwards, "
+                          f"FP32 C++ restatement of reference src/cpu (AVX-512 8x32 GEMM tile), "
+                          f"{threads} OpenMP threads")
+        gs, rs = batch.split_scores(gpu_scores), batch.split_scores(ref)
+        parity = dict(max_dlogit=float(np.abs(gpu_scores - ref).max()),
+                      argmax_agree=sum(int(np.argmax(a) == np.argmax(b)) for a, b in zip(gs, rs)), rows=len(gs))
+        log(f"cpu oracle: {med:.2f} s/forward on {threads} threads; parity {parity}")
+
+    out = {
+        "metric": METRIC, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded ids, random-init N(0,0.02) weights)",
+        "config": {"workload": args.workload, "shape": "ModernBERT-base encoder (22 layers, hidden 768, 12x64 heads, "
+                   "GEGLU 1152, local window 128 / global every 3rd) + 2 decision-head layers + scorer",
+                   "rows": int(batch.lens.size), "tokens": tokens, "markers": markers,
+                   "parallelism": "single GPU"},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "gemm_mfma_util_pct": round(gemm_util, 2),
+        "profiled_ms_per_step": round(prof_step_ms, 4),
+        "forward_with_pcie_ms": round(fwd_ms, 4),
+        "kernels": kern,
+        "parity_vs_cpu": parity,
+        **extra,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

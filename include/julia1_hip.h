@@ -132,7 +132,9 @@ int jh_forward_padded(jh_model* model, const uint32_t* ids, size_t batch, size_t
 
 /*
  * Split form of jh_forward, for callers that time or overlap the forward:
- *  jh_stage   validates and uploads the batch and blocks until it is resident;
+ *  jh_stage   validates the batch and enqueues its upload on the model's stream
+ *             (waiting first for earlier work that may still read the pinned
+ *             staging buffer);
  *  jh_execute enqueues the whole forward on the model's stream, reading the
  *             staged batch (repeatable; does not synchronise);
  *  jh_scores  waits for the stream and copies the M scores to the host.
@@ -152,6 +154,29 @@ void* jh_stream(jh_model* model);
  * while the staged shape is unchanged.  No reference counterpart.
  */
 int jh_set_graph(jh_model* model, int enabled);
+
+/*
+ * Per-kernel timing.  While profiling is enabled, jh_execute runs the launch
+ * sequence eagerly (no graph) and brackets every launch with a pair of HIP
+ * events on the model's stream.  jh_profile_read synchronises, sums the
+ * device time, launch count and algorithmic FLOPs/bytes per kernel class
+ * ("gemm_qkv_rope", "attn_global", ...) since the last read, and resets.
+ * It writes at most `capacity` entries and sets *count to the number of
+ * classes with launches.  No reference counterpart (the reference's CPU path
+ * has JULIA_PROFILE wall-clock slots, src/cpu/mod.rs:95-128).
+ */
+typedef struct jh_kernel_stat {
+    const char* name;
+    uint32_t launches;
+    double ms;       /* summed device time of the launches                  */
+    double flops;    /* algorithmic FLOPs: 2·M·N·K per GEMM, 4·64·heads per  */
+                     /* attended (query, key) pair                          */
+    double bytes;    /* algorithmic HBM bytes: operands read once, outputs  */
+                     /* written once (FP32 residual read and written)       */
+} jh_kernel_stat;
+
+int jh_profile(jh_model* model, int enabled);
+int jh_profile_read(jh_model* model, jh_kernel_stat* out, size_t capacity, size_t* count);
 
 /* "hip:N (<device name>)" — replaces `CudaModel::name` (src/cuda/mod.rs:252,278-280). */
 const char* jh_name(jh_model* model);

@@ -103,6 +103,32 @@ struct HeadLayer {
 
 constexpr int QTILE = 64;  // queries per attention work item
 
+// Kernel classes of the launch sequence, for jh_profile_read.
+enum KClass {
+    K_EMBED, K_LN, K_QKV, K_ATTN_GLOBAL, K_ATTN_LOCAL, K_WO, K_WI, K_WO2, K_FINAL,
+    K_HEAD_GEMM, K_HEAD_ATTN, K_HEAD_ROWS, K_SCORER, K_COUNT
+};
+const char* const kClassNames[K_COUNT] = {
+    "embed_ln", "layer_norm", "gemm_qkv_rope", "attn_global", "attn_local", "gemm_wo_resid", "gemm_wi_geglu",
+    "gemm_wo2_resid", "final_norm", "head_gemm", "head_attn", "head_rows", "scorer"};
+
+struct ProfRec {
+    int cls;
+    double flops, bytes;
+    hipEvent_t a, b;
+};
+
+double gemm_bytes(int epi, double rows, double n, double k) {
+    double out = 0;
+    switch (epi) {
+        case JH_EPI_GEGLU_BF16: out = rows * n / 2 * 2; break;
+        case JH_EPI_RESID_F32: out = rows * n * 8; break;
+        case JH_EPI_BIAS_F32: out = rows * n * 4; break;
+        default: out = rows * n * 2;
+    }
+    return rows * k * 2 + n * k * 2 + out;
+}
+
 }  // namespace
 
 struct jh_model {
@@ -136,10 +162,40 @@ struct jh_model {
     hipGraphExec_t graph = nullptr;
     size_t graph_key[6] = {0, 0, 0, 0, 0, 0};
     std::string name;
+    // attention (query, key) pairs of the staged batch, for algorithmic FLOPs
+    double pairs_global = 0, pairs_local = 0, pairs_marker = 0;
+    // profiling: one event pair per launch while enabled
+    bool profiling = false;
+    std::vector<hipEvent_t> ev_pool;
+    size_t ev_next = 0;
+    std::vector<ProfRec> recs;
 
     ~jh_model() {
         if (graph) (void)hipGraphExecDestroy(graph);
+        for (hipEvent_t e : ev_pool) (void)hipEventDestroy(e);
         if (stream) (void)hipStreamDestroy(stream);
+    }
+
+    hipEvent_t next_event() {
+        if (ev_next == ev_pool.size()) {
+            hipEvent_t e;
+            HIP_CHECK(hipEventCreate(&e));
+            ev_pool.push_back(e);
+        }
+        return ev_pool[ev_next++];
+    }
+
+    template <class F>
+    void timed(int cls, double flops, double bytes, F&& launch) {
+        if (!profiling) {
+            launch();
+            return;
+        }
+        ProfRec r{cls, flops, bytes, next_event(), next_event()};
+        HIP_CHECK(hipEventRecord(r.a, stream));
+        launch();
+        HIP_CHECK(hipEventRecord(r.b, stream));
+        recs.push_back(r);
     }
 
     void bind() const { HIP_CHECK(hipSetDevice(device)); }
@@ -228,6 +284,14 @@ struct jh_model {
         d_tiles = (AttnTile*)(dm + 2 * t);
         d_mtiles = (AttnTile*)(dm + 2 * t + 5 * tiles.size());
         d_markers = (int32_t*)(dm + 2 * t + 5 * (tiles.size() + mtiles.size()));
+        pairs_global = pairs_local = pairs_marker = 0;
+        for (size_t sq = 0; sq < nseq; ++sq) {
+            const double n = lens[sq];
+            pairs_global += n * n;
+            const long w = half_window, len = (long)lens[sq];
+            for (long i = 0; i < len; ++i) pairs_local += (double)(std::min(i + w, len - 1) - std::max(i - w, 0L) + 1);
+        }
+        for (const AttnTile& mt : mtiles) pairs_marker += (double)mt.nq * mt.kv_len;
         T = t;
         S = nseq;
         M = m;
@@ -236,40 +300,50 @@ struct jh_model {
         staged = true;
     }
 
-    void gemm(int epi, const void* xp, long ldx, const int32_t* gather, size_t rows, const DevBuf& w, int n, int k,
-              void* out, long ldo, int col, const float* bias, const float* cos_t = nullptr,
+    void gemm(int cls, int epi, const void* xp, long ldx, const int32_t* gather, size_t rows, const bf16_t* w, int n,
+              int k, void* out, long ldo, int col, const float* bias, const float* cos_t = nullptr,
               const float* sin_t = nullptr, int rope_cols = 0) {
-        GemmArgs a{(const bf16_t*)xp, ldx, gather, (int)rows, w.as<bf16_t>(), n, k, out, ldo, col, bias,
+        GemmArgs a{(const bf16_t*)xp, ldx, gather, (int)rows, w, n, k, out, ldo, col, bias,
                    (const int32_t*)d_tok, cos_t, sin_t, rope_cols};
-        launch_gemm(epi, a, stream);
+        timed(cls, 2.0 * rows * n * k, gemm_bytes(epi, rows, n, k), [&] { launch_gemm(epi, a, stream); });
     }
 
-    void attention(const bf16_t* q, long ldq, const bf16_t* k, const bf16_t* v, long ldkv, bf16_t* out, long ldo,
-                   const AttnTile* tiles, size_t n, int nheads, int window) {
+    void attention(int cls, const bf16_t* q, long ldq, const bf16_t* k, const bf16_t* v, long ldkv, bf16_t* out,
+                   long ldo, const AttnTile* tiles, size_t n, int nheads, int window, double pairs, double qrows) {
         AttnArgs a{q, ldq, k, v, ldkv, out, ldo, tiles, (int)n, nheads, window, 0.125f * 1.4426950408889634f};
-        launch_attention(a, stream);
+        const double hd = 64.0 * nheads;
+        timed(cls, 4.0 * hd * pairs, qrows * hd * 2 * 2 + (double)T * hd * 2 * 2, [&] { launch_attention(a, stream); });
+    }
+
+    void layer_norm(int cls, const float* xp, size_t rows, const float* w, const float* b, float e, bf16_t* out) {
+        timed(cls, 0, (double)rows * h * 6, [&] { launch_layer_norm(xp, (int)rows, w, b, e, h, out, stream); });
     }
 
     // Embeddings and the first `upto` encoder layers (src/cuda/mod.rs:446-463).
     void run_encoder(int upto) {
         const int H = h;
         const size_t t = T;
-        launch_embed_ln(d_ids, (int)t, emb.as<float>(), emb_norm.as<float>(), eps, H, x.as<float>(), xn.as<bf16_t>(),
-                        stream);
+        timed(K_EMBED, 0, (double)t * (H * 10 + 4), [&] {
+            launch_embed_ln(d_ids, (int)t, emb.as<float>(), emb_norm.as<float>(), eps, H, x.as<float>(),
+                            xn.as<bf16_t>(), stream);
+        });
         for (int l = 0; l < upto; ++l) {
             EncLayer& L = layers[l];
-            if (L.attn_norm.p)
-                launch_layer_norm(x.as<float>(), (int)t, L.attn_norm.as<float>(), nullptr, eps, H, xn.as<bf16_t>(),
-                                  stream);
-            gemm(JH_EPI_ROPE_BF16, xn.p, H, nullptr, t, L.wqkv, 3 * H, H, qkv.p, 3 * H, 0, nullptr,
+            if (L.attn_norm.p) layer_norm(K_LN, x.as<float>(), t, L.attn_norm.as<float>(), nullptr, eps, xn.as<bf16_t>());
+            gemm(K_QKV, JH_EPI_ROPE_BF16, xn.p, H, nullptr, t, L.wqkv.as<bf16_t>(), 3 * H, H, qkv.p, 3 * H, 0, nullptr,
                  ropes[L.rope].first.as<float>(), ropes[L.rope].second.as<float>(), 2 * H);
             const bf16_t* q = qkv.as<bf16_t>();
-            attention(q, 3 * H, q + H, q + 2 * H, 3 * H, ctx.as<bf16_t>(), H, d_tiles, ntiles, heads,
-                      L.global ? -1 : half_window);
-            gemm(JH_EPI_RESID_F32, ctx.p, H, nullptr, t, L.wo, H, H, x.p, H, 0, nullptr);
-            launch_layer_norm(x.as<float>(), (int)t, L.mlp_norm.as<float>(), nullptr, eps, H, xn.as<bf16_t>(), stream);
-            gemm(JH_EPI_GEGLU_BF16, xn.p, H, nullptr, t, L.wi, 2 * inter, H, hbuf.p, inter, 0, nullptr);
-            gemm(JH_EPI_RESID_F32, hbuf.p, inter, nullptr, t, L.wo2, H, inter, x.p, H, 0, nullptr);
+            if (L.global)
+                attention(K_ATTN_GLOBAL, q, 3 * H, q + H, q + 2 * H, 3 * H, ctx.as<bf16_t>(), H, d_tiles, ntiles, heads,
+                          -1, pairs_global, (double)t);
+            else
+                attention(K_ATTN_LOCAL, q, 3 * H, q + H, q + 2 * H, 3 * H, ctx.as<bf16_t>(), H, d_tiles, ntiles, heads,
+                          half_window, pairs_local, (double)t);
+            gemm(K_WO, JH_EPI_RESID_F32, ctx.p, H, nullptr, t, L.wo.as<bf16_t>(), H, H, x.p, H, 0, nullptr);
+            layer_norm(K_LN, x.as<float>(), t, L.mlp_norm.as<float>(), nullptr, eps, xn.as<bf16_t>());
+            gemm(K_WI, JH_EPI_GEGLU_BF16, xn.p, H, nullptr, t, L.wi.as<bf16_t>(), 2 * inter, H, hbuf.p, inter, 0,
+                 nullptr);
+            gemm(K_WO2, JH_EPI_RESID_F32, hbuf.p, inter, nullptr, t, L.wo2.as<bf16_t>(), H, inter, x.p, H, 0, nullptr);
         }
     }
 
@@ -279,44 +353,56 @@ struct jh_model {
         const int H = h;
         const size_t t = T, m = M;
         const int nh = (int)head.size();
-        launch_final_norm(x.as<float>(), (int)t, final_norm.as<float>(), type_emb.as<float>(), d_tok,
-                          head[0].norm1_w.as<float>(), head[0].norm1_b.as<float>(), eps, H, xn.as<bf16_t>(), stream);
+        timed(K_FINAL, 0, (double)t * (H * 10 + 4), [&] {
+            launch_final_norm(x.as<float>(), (int)t, final_norm.as<float>(), type_emb.as<float>(), d_tok,
+                              head[0].norm1_w.as<float>(), head[0].norm1_b.as<float>(), eps, H, xn.as<bf16_t>(),
+                              stream);
+        });
         for (int j = 0; j + 1 < nh; ++j) {
             HeadLayer& L = head[j];
-            gemm(JH_EPI_BIAS_BF16, xn.p, H, nullptr, t, L.in_w, 3 * H, H, qkv.p, 3 * H, 0, L.in_b.as<float>());
+            gemm(K_HEAD_GEMM, JH_EPI_BIAS_BF16, xn.p, H, nullptr, t, L.in_w.as<bf16_t>(), 3 * H, H, qkv.p, 3 * H, 0,
+                 L.in_b.as<float>());
             const bf16_t* q = qkv.as<bf16_t>();
-            attention(q, 3 * H, q + H, q + 2 * H, 3 * H, ctx.as<bf16_t>(), H, d_tiles, ntiles, head_heads, -1);
-            gemm(JH_EPI_RESID_F32, ctx.p, H, nullptr, t, L.out_w, H, H, x.p, H, 0, L.out_b.as<float>());
-            launch_layer_norm(x.as<float>(), (int)t, L.norm2_w.as<float>(), L.norm2_b.as<float>(), 1e-5f, H,
-                              xn.as<bf16_t>(), stream);
-            gemm(JH_EPI_BIAS_RELU_BF16, xn.p, H, nullptr, t, L.lin1_w, ff, H, hbuf.p, ff, 0, L.lin1_b.as<float>());
-            gemm(JH_EPI_RESID_F32, hbuf.p, ff, nullptr, t, L.lin2_w, H, ff, x.p, H, 0, L.lin2_b.as<float>());
+            attention(K_HEAD_ATTN, q, 3 * H, q + H, q + 2 * H, 3 * H, ctx.as<bf16_t>(), H, d_tiles, ntiles, head_heads,
+                      -1, pairs_global, (double)t);
+            gemm(K_HEAD_GEMM, JH_EPI_RESID_F32, ctx.p, H, nullptr, t, L.out_w.as<bf16_t>(), H, H, x.p, H, 0,
+                 L.out_b.as<float>());
+            layer_norm(K_HEAD_ROWS, x.as<float>(), t, L.norm2_w.as<float>(), L.norm2_b.as<float>(), 1e-5f,
+                       xn.as<bf16_t>());
+            gemm(K_HEAD_GEMM, JH_EPI_BIAS_RELU_BF16, xn.p, H, nullptr, t, L.lin1_w.as<bf16_t>(), ff, H, hbuf.p, ff, 0,
+                 L.lin1_b.as<float>());
+            gemm(K_HEAD_GEMM, JH_EPI_RESID_F32, hbuf.p, ff, nullptr, t, L.lin2_w.as<bf16_t>(), H, ff, x.p, H, 0,
+                 L.lin2_b.as<float>());
             HeadLayer& N = head[j + 1];
-            launch_layer_norm(x.as<float>(), (int)t, N.norm1_w.as<float>(), N.norm1_b.as<float>(), 1e-5f, H,
-                              xn.as<bf16_t>(), stream);
+            layer_norm(K_HEAD_ROWS, x.as<float>(), t, N.norm1_w.as<float>(), N.norm1_b.as<float>(), 1e-5f,
+                       xn.as<bf16_t>());
         }
         HeadLayer& L = head[nh - 1];
         // Keys/values for every token: in_proj rows [H, 3H) into qkv columns [H, 3H).
-        {
-            GemmArgs a{xn.as<bf16_t>(), H, nullptr, (int)t, L.in_w.as<bf16_t>() + (size_t)H * H, 2 * H, H, qkv.p,
-                       3 * H, H, L.in_b.as<float>() + H, nullptr, nullptr, nullptr, 0};
-            launch_gemm(JH_EPI_BIAS_BF16, a, stream);
-        }
+        gemm(K_HEAD_GEMM, JH_EPI_BIAS_BF16, xn.p, H, nullptr, t, L.in_w.as<bf16_t>() + (size_t)H * H, 2 * H, H, qkv.p,
+             3 * H, H, L.in_b.as<float>() + H);
         // Queries for markers only, gathered straight from the normed rows.
-        gemm(JH_EPI_BIAS_BF16, xn.p, H, d_markers, m, L.in_w, H, H, qm.p, H, 0, L.in_b.as<float>());
+        gemm(K_HEAD_GEMM, JH_EPI_BIAS_BF16, xn.p, H, d_markers, m, L.in_w.as<bf16_t>(), H, H, qm.p, H, 0,
+             L.in_b.as<float>());
         const bf16_t* kv = qkv.as<bf16_t>();
-        attention(qm.as<bf16_t>(), H, kv + H, kv + 2 * H, 3 * H, cm.as<bf16_t>(), H, d_mtiles, nmtiles, head_heads, -1);
-        launch_gather_f32(x.as<float>(), d_markers, (int)m, H, y.as<float>(), stream);
-        gemm(JH_EPI_RESID_F32, cm.p, H, nullptr, m, L.out_w, H, H, y.p, H, 0, L.out_b.as<float>());
-        launch_layer_norm(y.as<float>(), (int)m, L.norm2_w.as<float>(), L.norm2_b.as<float>(), 1e-5f, H,
-                          yn.as<bf16_t>(), stream);
-        gemm(JH_EPI_BIAS_RELU_BF16, yn.p, H, nullptr, m, L.lin1_w, ff, H, hm.p, ff, 0, L.lin1_b.as<float>());
-        gemm(JH_EPI_RESID_F32, hm.p, ff, nullptr, m, L.lin2_w, H, ff, y.p, H, 0, L.lin2_b.as<float>());
+        attention(K_HEAD_ATTN, qm.as<bf16_t>(), H, kv + H, kv + 2 * H, 3 * H, cm.as<bf16_t>(), H, d_mtiles, nmtiles,
+                  head_heads, -1, pairs_marker, (double)m);
+        timed(K_HEAD_ROWS, 0, (double)m * H * 8, [&] {
+            launch_gather_f32(x.as<float>(), d_markers, (int)m, H, y.as<float>(), stream);
+        });
+        gemm(K_HEAD_GEMM, JH_EPI_RESID_F32, cm.p, H, nullptr, m, L.out_w.as<bf16_t>(), H, H, y.p, H, 0,
+             L.out_b.as<float>());
+        layer_norm(K_HEAD_ROWS, y.as<float>(), m, L.norm2_w.as<float>(), L.norm2_b.as<float>(), 1e-5f, yn.as<bf16_t>());
+        gemm(K_HEAD_GEMM, JH_EPI_BIAS_RELU_BF16, yn.p, H, nullptr, m, L.lin1_w.as<bf16_t>(), ff, H, hm.p, ff, 0,
+             L.lin1_b.as<float>());
+        gemm(K_HEAD_GEMM, JH_EPI_RESID_F32, hm.p, ff, nullptr, m, L.lin2_w.as<bf16_t>(), H, ff, y.p, H, 0,
+             L.lin2_b.as<float>());
         // Scorer: LayerNorm -> Linear -> GELU -> Linear(.., 1).
-        launch_layer_norm(y.as<float>(), (int)m, s_norm_w.as<float>(), s_norm_b.as<float>(), 1e-5f, H,
-                          yn.as<bf16_t>(), stream);
-        gemm(JH_EPI_BIAS_F32, yn.p, H, nullptr, m, s_w1, H, H, z.p, H, 0, s_b1.as<float>());
-        launch_scorer(z.as<float>(), (int)m, H, s_w2.as<float>(), s_b2, scores.as<float>(), stream);
+        layer_norm(K_SCORER, y.as<float>(), m, s_norm_w.as<float>(), s_norm_b.as<float>(), 1e-5f, yn.as<bf16_t>());
+        gemm(K_SCORER, JH_EPI_BIAS_F32, yn.p, H, nullptr, m, s_w1.as<bf16_t>(), H, H, z.p, H, 0, s_b1.as<float>());
+        timed(K_SCORER, 4.0 * m * H, (double)m * H * 4 + m * 4.0, [&] {
+            launch_scorer(z.as<float>(), (int)m, H, s_w2.as<float>(), s_b2, scores.as<float>(), stream);
+        });
     }
 
     void run_all() {
@@ -328,7 +414,7 @@ struct jh_model {
     void execute() {
         if (!staged) throw jh_error(JH_ERR_INVALID, "no batch staged");
         if (T == 0 || M == 0) return;
-        if (!use_graph) {
+        if (!use_graph || profiling) {
             run_all();
             return;
         }
@@ -413,7 +499,11 @@ void build_model(jh_model* m, const jh_config* c, const jh_weights* w, int ordin
     m->bind();
     hipDeviceProp_t prop;
     HIP_CHECK(hipGetDeviceProperties(&prop, ordinal));
-    m->name = "hip:" + std::to_string(ordinal) + " (" + prop.name + ")";
+    // prop.name can be blank when the marketing-name table is absent; the gfx arch is always set.
+    std::string dev_name = prop.name[0] ? prop.name : "AMD GPU";
+    std::string arch = prop.gcnArchName;
+    arch = arch.substr(0, arch.find(':'));
+    m->name = "hip:" + std::to_string(ordinal) + " (" + dev_name + ", " + arch + ")";
     HIP_CHECK(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking));
     const size_t H = c->hidden, I = c->intermediate, F = c->head_ff;
     m->h = (int)H; m->heads = (int)c->heads; m->inter = (int)I; m->nlayers = (int)c->layers;
@@ -515,6 +605,46 @@ int jh_set_graph(jh_model* model, int enabled) {
         if (!model) throw jh_error(JH_ERR_INVALID, "null model");
         std::lock_guard<std::mutex> g(model->mu);
         model->use_graph = enabled != 0;
+    });
+}
+
+int jh_profile(jh_model* model, int enabled) {
+    return jh_guarded([&] {
+        if (!model) throw jh_error(JH_ERR_INVALID, "null model");
+        std::lock_guard<std::mutex> g(model->mu);
+        model->bind();
+        HIP_CHECK(hipStreamSynchronize(model->stream));
+        model->profiling = enabled != 0;
+        model->recs.clear();
+        model->ev_next = 0;
+    });
+}
+
+int jh_profile_read(jh_model* model, jh_kernel_stat* out, size_t capacity, size_t* count) {
+    return jh_guarded([&] {
+        if (!model || !count) throw jh_error(JH_ERR_INVALID, "null argument");
+        std::lock_guard<std::mutex> g(model->mu);
+        model->bind();
+        HIP_CHECK(hipStreamSynchronize(model->stream));
+        jh_kernel_stat acc[K_COUNT];
+        for (int c = 0; c < K_COUNT; ++c) acc[c] = jh_kernel_stat{kClassNames[c], 0, 0.0, 0.0, 0.0};
+        for (const ProfRec& r : model->recs) {
+            float ms = 0.0f;
+            HIP_CHECK(hipEventElapsedTime(&ms, r.a, r.b));
+            acc[r.cls].launches += 1;
+            acc[r.cls].ms += ms;
+            acc[r.cls].flops += r.flops;
+            acc[r.cls].bytes += r.bytes;
+        }
+        model->recs.clear();
+        model->ev_next = 0;
+        size_t n = 0;
+        for (int c = 0; c < K_COUNT; ++c) {
+            if (!acc[c].launches) continue;
+            if (out && n < capacity) out[n] = acc[c];
+            ++n;
+        }
+        *count = n;
     });
 }
 

@@ -18,10 +18,15 @@ _lib = None
 EXPORTS = (
     "jh_create", "jh_forward", "jh_forward_padded", "jh_stage", "jh_execute", "jh_scores", "jh_stream",
     "jh_set_graph", "jh_name", "jh_destroy", "jh_last_error", "jh_rope_table", "jh_debug_tokens",
-    "jh_debug_encode",
+    "jh_debug_encode", "jh_profile", "jh_profile_read",
     "jh_op_gemm", "jh_op_interleave_geglu", "jh_op_embed_ln", "jh_op_layer_norm", "jh_op_final_norm",
     "jh_op_gather_f32", "jh_op_scorer", "jh_op_attention",
 )
+
+
+class KernelStat(C.Structure):
+    _fields_ = [("name", C.c_char_p), ("launches", C.c_uint32), ("ms", C.c_double), ("flops", C.c_double),
+                ("bytes", C.c_double)]
 
 
 class HipError(RuntimeError):
@@ -56,6 +61,8 @@ def lib():
         L.jh_rope_table.restype = None
         L.jh_debug_tokens.argtypes = [vp, vp, vp, sz]
         L.jh_debug_encode.argtypes = [vp, u32, vp, sz]
+        L.jh_profile.argtypes = [vp, C.c_int]
+        L.jh_profile_read.argtypes = [vp, vp, sz, C.POINTER(sz)]
         L.jh_op_gemm.argtypes = [C.c_int, vp, sz, vp, sz, vp, sz, sz, vp, sz, sz, vp, vp, vp, vp, sz, vp]
         L.jh_op_interleave_geglu.argtypes = [vp, sz, sz, vp]
         L.jh_op_interleave_geglu.restype = None
@@ -148,6 +155,17 @@ class HipModel:
         x = np.zeros((t, self.cfg.hidden), dtype=np.float32)
         check(lib().jh_debug_encode(self.h, layers, _p(x), t))
         return x
+
+    def profile(self, on: bool):
+        check(lib().jh_profile(self.h, 1 if on else 0))
+
+    def profile_read(self) -> list:
+        """[{name, launches, ms, flops, bytes}] summed since the last read (device time from HIP events)."""
+        arr = (KernelStat * 32)()
+        n = C.c_size_t()
+        check(lib().jh_profile_read(self.h, arr, 32, C.byref(n)))
+        return [dict(name=arr[i].name.decode(), launches=arr[i].launches, ms=arr[i].ms, flops=arr[i].flops,
+                     bytes=arr[i].bytes) for i in range(n.value)]
 
     def close(self):
         if getattr(self, "h", None) and _lib is not None:

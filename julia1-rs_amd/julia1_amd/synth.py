@@ -142,8 +142,9 @@ class SplitMix64:
 
 
 def marker_positions(length: int, n: int) -> list:
+    """n option-marker positions spread over the row, clamped inside it."""
     step = max(1, (length - 2) // n)
-    return [1 + j * step for j in range(n)]
+    return [min(1 + j * step, length - 1) for j in range(n)]
 
 
 def make_batch(lens, n_options, vocab: int, seed: int) -> Batch:

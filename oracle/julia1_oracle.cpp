@@ -565,6 +565,9 @@ void jo_set_threads(jo_model* m, int threads) { if (m && threads > 0) m->threads
 
 void jo_set_fault(int code) { g_fault = code; }
 
+// Thread count of the op-level entry points (jo_linear, jo_attention, ...).
+void jo_omp_threads(int n) { if (n > 0) omp_set_num_threads(n); }
+
 static bool check_batch(jo_model* m, const uint32_t* ids, size_t t, const uint32_t* starts, const uint32_t* lens, size_t S,
                         const uint32_t* marker_rows, size_t M) {
     size_t next = 0;

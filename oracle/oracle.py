@@ -33,6 +33,7 @@ def lib():
         L.jo_destroy.argtypes = [vp]
         L.jo_set_threads.argtypes = [vp, C.c_int]
         L.jo_set_fault.argtypes = [C.c_int]
+        L.jo_omp_threads.argtypes = [C.c_int]
         L.jo_forward.argtypes = [vp, vp, sz, vp, vp, vp, sz, vp, sz, vp]
         L.jo_encode.argtypes = [vp, vp, sz, vp, vp, sz, C.c_uint32, vp]
         for n in ("jo_exp", "jo_erf", "jo_gelu"):
@@ -94,6 +95,11 @@ class OracleModel:
         if getattr(self, "h", None) and _lib is not None:
             _lib.jo_destroy(self.h)
             self.h = None
+
+
+def omp_threads(n: int):
+    """Thread count of the op-level functions below."""
+    lib().jo_omp_threads(n)
 
 
 def set_fault(code: int):

@@ -1,0 +1,120 @@
+"""Host-side checks that need no GPU: the C-ABI library loads and exports
+every function include/*.h declares; the config parser restates
+ModelConfig::from_values; the synthetic generators are deterministic."""
+import os
+import re
+
+import numpy as np
+import pytest
+
+from julia1_amd import abi, hip, synth
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_functions():
+    names = []
+    for f in sorted(os.listdir(os.path.join(ROOT, "include"))):
+        if f.endswith(".h"):
+            text = open(os.path.join(ROOT, "include", f)).read()
+            text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+            names += re.findall(r"^\s*(?:const\s+)?[\w]+\s*\**\s*(j[he]_\w+)\s*\(", text, flags=re.M)
+    return sorted(set(names))
+
+
+def test_library_exports_every_declared_symbol():
+    names = declared_functions()
+    assert len(names) >= 20
+    lib = hip.lib()
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    assert set(hip.EXPORTS) <= set(names)
+
+
+def test_last_error_is_empty_string_initially():
+    assert hip.lib().jh_last_error() is not None
+
+
+def test_create_without_device_reports_error_not_crash():
+    torch = pytest.importorskip("torch")
+    if torch.cuda.device_count() > 0:
+        pytest.skip("a GPU is present; covered by the GPU tests")
+    cfg = synth.model_config("tiny")
+    ws = abi.WeightSet(cfg, synth.make_weights(cfg, 0))
+    with pytest.raises(hip.HipError) as e:
+        hip.HipModel(ws)
+    assert e.value.code == 2
+
+
+def test_create_rejects_bad_config_before_touching_device():
+    cfg = synth.model_config("tiny")
+    ws = abi.WeightSet(cfg, synth.make_weights(cfg, 0))
+    ws.config.head_dim = 32
+    with pytest.raises(hip.HipError) as e:
+        hip.HipModel(ws)
+    assert e.value.code == 1
+
+
+def test_config_from_values_base():
+    c = synth.model_config("modernbert-base")
+    assert (c.hidden, c.heads, c.head_dim, c.intermediate, c.layers) == (768, 12, 64, 1152, 22)
+    assert c.global_ == [i % 3 == 0 for i in range(22)] and sum(c.global_) == 8
+    assert c.half_window == 64 and c.head_ff == 3072 and c.head_heads == 12
+    assert c.rope_theta == [160000.0 if i % 3 == 0 else 10000.0 for i in range(22)]
+
+
+def test_config_rejections():
+    s = synth.SHAPES["tiny"]
+    for key, val in (("hidden_activation", "relu"), ("norm_bias", True), ("model_type", "bert")):
+        enc = dict(s["enc"], **{key: val})
+        with pytest.raises(ValueError):
+            abi.ModelConfig.from_values(s["julia"], enc)
+    with pytest.raises(ValueError):
+        abi.ModelConfig.from_values(dict(s["julia"], format_version=2), s["enc"])
+    with pytest.raises(ValueError):
+        abi.ModelConfig.from_values(dict(s["julia"], weight_dtype="int8"), s["enc"])
+    enc = dict(s["enc"], hidden_size=96, num_attention_heads=2)
+    with pytest.raises(ValueError):
+        abi.ModelConfig.from_values(s["julia"], enc)
+
+
+def test_rope_parameters_override():
+    s = synth.SHAPES["tiny"]
+    enc = dict(s["enc"], rope_parameters={"full_attention": {"rope_type": "default", "rope_theta": 5e5},
+                                          "sliding_attention": {"rope_type": "default", "rope_theta": 2e4}})
+    c = abi.ModelConfig.from_values(s["julia"], enc)
+    assert c.rope_theta == [5e5, 2e4, 2e4]
+
+
+def test_workloads_are_deterministic_and_shaped():
+    b1 = synth.workload("config1")
+    b1b = synth.workload("config1")
+    assert np.array_equal(b1.ids, b1b.ids) and np.array_equal(b1.marker_rows, b1b.marker_rows)
+    assert b1.lens.size == 32 and b1.lens.min() >= 64 and b1.lens.max() <= 512
+    opts = np.diff(b1.marker_starts)
+    assert opts.min() >= 2 and opts.max() <= 20
+    assert b1.ids.max() < 50368
+    b4 = synth.workload("config4")
+    assert b4.lens.size == 256 and 32 <= b4.lens.min() and b4.lens.max() <= 1024
+    assert 120_000 < b4.tokens < 150_000 and b4.marker_rows.size == 5120
+    for b in (b1, b4):
+        for s in range(b.lens.size):
+            rows = b.marker_rows[b.marker_starts[s]:b.marker_starts[s + 1]]
+            assert np.all((rows >= b.starts[s]) & (rows < b.starts[s] + b.lens[s]))
+
+
+def test_padded_round_trip():
+    b = synth.workload("config1").subset(range(5))
+    ids, lens, qt, markers, mst = synth.padded(b, 512)
+    assert ids.shape == (5, 512)
+    for s in range(5):
+        assert np.array_equal(ids[s, :lens[s]], b.ids[b.starts[s]:b.starts[s] + lens[s]])
+
+
+def test_interleave_geglu_layout():
+    inter, k = 96, 5
+    wi = np.arange(2 * inter * k, dtype=np.float32).reshape(2 * inter, k)
+    out = hip.interleave_geglu(wi)
+    for j in range(inter // 32):
+        assert np.array_equal(out[64 * j:64 * j + 32], wi[32 * j:32 * j + 32])
+        assert np.array_equal(out[64 * j + 32:64 * j + 64], wi[inter + 32 * j:inter + 32 * j + 32])
