@@ -8,12 +8,18 @@
 // what the epilogues want: 16-byte FP32 residual read-modify-writes, and the
 // RoPE pair (d, d+32) and the GEGLU pair (gate, up) in the same lane.
 //
-// Workgroup tile BF features x BT tokens x BK=64, LDS double-buffered with
-// register prefetch (one barrier per K step).  LDS rows are padded to 72
-// bf16 (144 B) so the 16-byte fragment reads of 8 consecutive rows hit
-// distinct banks.  Tiles are assigned XCD-contiguously: MI355X deals
-// workgroups round-robin to its 8 XCDs, so tile t is given to workgroup
-// b with b % 8 = XCD, keeping each XCD's L2 on a contiguous band of tokens.
+// Pipeline: workgroup tile BF features x BT tokens x BK=64.  Global loads run
+// two K steps ahead of the MFMAs (two register stages), LDS is double
+// buffered, one barrier per K step.  At K = 768 that keeps 2/12 of the whole
+// operand stream in flight per workgroup, which hides the HBM/MALL latency.
+// All loads are unconditional (out-of-range rows are clamped) so the
+// compiler's vmcnt waits stay exact.  LDS rows are padded to 72 bf16 (144 B)
+// so the 16-byte fragment reads of 8 consecutive rows hit distinct banks.
+//
+// Tiles are dealt XCD-contiguously: MI355X hands workgroups round-robin to its
+// 8 XCDs, so tile t goes to the workgroup whose id mod 8 selects the XCD that
+// owns t's band; inside a band, tiles are grouped 8 token blocks at a time so
+// the operands resident on one XCD fit its 4 MB L2.
 #include <hip/hip_runtime.h>
 
 #include "../../include/julia1_hip_ops.h"
@@ -24,117 +30,18 @@ namespace {
 constexpr int BK = 64;
 constexpr int LDS_STRIDE = 72;
 
-template <int EPI, int BF, int BT, int WF, int WT>
-__global__ __launch_bounds__(WF* WT * 64) void gemm_kernel(GemmArgs a) {
-    constexpr int NT = WF * WT * 64;
-    constexpr int FPW = BF / WF, TPW = BT / WT;  // features / tokens per wave
-    constexpr int FB = FPW / 32, TB = TPW / 32;  // 32x32 MFMA blocks per wave
-    constexpr int CW = BF * 8 / NT, CX = BT * 8 / NT;  // 16-byte chunks per thread per K step
-    static_assert(CW * NT == BF * 8 && CX * NT == BT * 8, "tile must split evenly over threads");
-    static_assert(FB >= 1 && TB >= 1, "wave tile too small");
-    static_assert((EPI != JH_EPI_ROPE_BF16 && EPI != JH_EPI_GEGLU_BF16) || FB % 2 == 0,
-                  "pair epilogues need 64-feature wave slabs");
-
-    __shared__ __align__(16) bf16_t sW[2][BF][LDS_STRIDE];
-    __shared__ __align__(16) bf16_t sX[2][BT][LDS_STRIDE];
-
-    const int tid = threadIdx.x;
-    const int nF = (a.n + BF - 1) / BF;
-    const int nTk = (a.rows + BT - 1) / BT;
-    const int ntiles = nF * nTk;
-    const int b = blockIdx.x;
-    const int xcd = b & 7, local = b >> 3, q8 = ntiles >> 3, r8 = ntiles & 7;
-    const int tile = xcd * q8 + (xcd < r8 ? xcd : r8) + local;
-    const int f0 = (tile % nF) * BF, t0 = (tile / nF) * BT;
-
-    // Per-thread source rows for the global->LDS copies (fixed across K steps).
-    const bf16_t* wsrc[CW];
-    const bf16_t* xsrc[CX];
-#pragma unroll
-    for (int i = 0; i < CW; ++i) {
-        int c = tid + NT * i, row = c >> 3, kc = c & 7;
-        int f = f0 + row;
-        wsrc[i] = f < a.n ? a.w + (long)f * a.k + kc * 8 : nullptr;
-    }
-#pragma unroll
-    for (int i = 0; i < CX; ++i) {
-        int c = tid + NT * i, row = c >> 3, kc = c & 7;
-        int t = t0 + row;
-        if (t < a.rows) {
-            long src = a.gather ? (long)a.gather[t] : (long)t;
-            xsrc[i] = a.x + src * a.ldx + kc * 8;
-        } else {
-            xsrc[i] = nullptr;
-        }
-    }
-
-    u32x4 rw[CW], rx[CX];
-    auto gload = [&](int kt) {
-        const int kb = kt * BK;
-#pragma unroll
-        for (int i = 0; i < CW; ++i) rw[i] = wsrc[i] ? *(const u32x4*)(wsrc[i] + kb) : u32x4{0, 0, 0, 0};
-#pragma unroll
-        for (int i = 0; i < CX; ++i) rx[i] = xsrc[i] ? *(const u32x4*)(xsrc[i] + kb) : u32x4{0, 0, 0, 0};
-    };
-    auto sstore = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < CW; ++i) {
-            int c = tid + NT * i;
-            *(u32x4*)&sW[buf][c >> 3][(c & 7) * 8] = rw[i];
-        }
-#pragma unroll
-        for (int i = 0; i < CX; ++i) {
-            int c = tid + NT * i;
-            *(u32x4*)&sX[buf][c >> 3][(c & 7) * 8] = rx[i];
-        }
-    };
-
-    const int lane = tid & 63, wave = tid >> 6;
-    const int wf = wave % WF, wt = wave / WF;
-    const int lr = lane & 31, lk = (lane >> 5) * 8;
-
-    f32x16 acc[FB][TB];
-#pragma unroll
-    for (int i = 0; i < FB; ++i)
-#pragma unroll
-        for (int j = 0; j < TB; ++j)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
-
-    const int KT = a.k / BK;
-    gload(0);
-    sstore(0);
-    __syncthreads();
-    for (int kt = 0; kt < KT; ++kt) {
-        const int buf = kt & 1;
-        if (kt + 1 < KT) gload(kt + 1);
-#pragma unroll
-        for (int ks = 0; ks < BK / 16; ++ks) {
-            bf16x8 af[FB], bx[TB];
-#pragma unroll
-            for (int i = 0; i < FB; ++i) af[i] = *(const bf16x8*)&sW[buf][wf * FPW + i * 32 + lr][ks * 16 + lk];
-#pragma unroll
-            for (int j = 0; j < TB; ++j) bx[j] = *(const bf16x8*)&sX[buf][wt * TPW + j * 32 + lr][ks * 16 + lk];
-#pragma unroll
-            for (int i = 0; i < FB; ++i)
-#pragma unroll
-                for (int j = 0; j < TB; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bx[j], acc[i][j], 0, 0, 0);
-        }
-        if (kt + 1 < KT) sstore(buf ^ 1);
-        __syncthreads();
-    }
-
-    // Epilogue.  acc[i][j][e]: feature fslab(i) + (e/4)*8 + g4 + e%4, token t(j).
-    const int g4 = (lane >> 5) * 4;
+template <int EPI, int FB, int TB>
+__device__ inline void epilogue(const GemmArgs& a, f32x16 (&acc)[FB][TB], int fw0, int tw0, int lane) {
+    // acc[i][j][e]: feature fw0 + i*32 + (e/4)*8 + g4 + e%4, token tw0 + j*32 + lr.
+    const int g4 = (lane >> 5) * 4, lr = lane & 31;
 #pragma unroll
     for (int j = 0; j < TB; ++j) {
-        const int t = t0 + wt * TPW + j * 32 + lr;
+        const int t = tw0 + j * 32 + lr;
         if (t >= a.rows) continue;
         if constexpr (EPI == JH_EPI_ROPE_BF16 || EPI == JH_EPI_GEGLU_BF16) {
 #pragma unroll
             for (int i = 0; i < FB; i += 2) {
-                const int slab = f0 + wf * FPW + i * 32;  // 64-aligned: [slab, slab+32) pairs with [slab+32, slab+64)
+                const int slab = fw0 + i * 32;  // 64-aligned: [slab, slab+32) pairs with [slab+32, slab+64)
                 if (slab >= a.n) continue;
                 if constexpr (EPI == JH_EPI_ROPE_BF16) {
                     bf16_t* o = (bf16_t*)a.out + (long)t * a.ldo + a.col + slab;
@@ -177,7 +84,7 @@ __global__ __launch_bounds__(WF* WT * 64) void gemm_kernel(GemmArgs a) {
         } else {
 #pragma unroll
             for (int i = 0; i < FB; ++i) {
-                const int slab = f0 + wf * FPW + i * 32;
+                const int slab = fw0 + i * 32;
                 if (slab >= a.n) continue;
 #pragma unroll
                 for (int qd = 0; qd < 4; ++qd) {
@@ -220,12 +127,148 @@ __global__ __launch_bounds__(WF* WT * 64) void gemm_kernel(GemmArgs a) {
     }
 }
 
+template <int EPI, int BF, int BT, int WF, int WT>
+__global__ __launch_bounds__(WF* WT * 64) void gemm_kernel(GemmArgs a) {
+    constexpr int NT = WF * WT * 64;
+    constexpr int FPW = BF / WF, TPW = BT / WT;  // features / tokens per wave
+    constexpr int FB = FPW / 32, TB = TPW / 32;  // 32x32 MFMA blocks per wave
+    constexpr int CW = BF * 8 / NT, CX = BT * 8 / NT;  // 16-byte chunks per thread per K step
+    static_assert(CW * NT == BF * 8 && CX * NT == BT * 8, "tile must split evenly over threads");
+    static_assert(FB >= 1 && TB >= 1, "wave tile too small");
+    static_assert((EPI != JH_EPI_ROPE_BF16 && EPI != JH_EPI_GEGLU_BF16) || FB % 2 == 0,
+                  "pair epilogues need 64-feature wave slabs");
+
+    __shared__ __align__(16) bf16_t sW[2][BF][LDS_STRIDE];
+    __shared__ __align__(16) bf16_t sX[2][BT][LDS_STRIDE];
+
+    const int tid = threadIdx.x;
+    const int nF = (a.n + BF - 1) / BF;
+    const int nTk = (a.rows + BT - 1) / BT;
+    const int ntiles = nF * nTk;
+    const int b = blockIdx.x;
+    const int xcd = b & 7, local = b >> 3, q8 = ntiles >> 3, r8 = ntiles & 7;
+    const int tile = xcd * q8 + (xcd < r8 ? xcd : r8) + local;
+    // Grouped order inside an XCD's band: GROUP token blocks are swept for
+    // each feature block, so the ~64 tiles resident on one XCD share about
+    // GROUP token blocks and 64/GROUP feature blocks of operands in its L2.
+    constexpr int GROUP = 8;
+    const int grp = tile / (GROUP * nF), gi = tile - grp * GROUP * nF;
+    const int gh = min(GROUP, nTk - grp * GROUP);
+    const int f0 = (gi / gh) * BF, t0 = (grp * GROUP + gi % gh) * BT;
+
+    // Per-thread source rows for the global->LDS copies (fixed across K steps).
+    // Rows past the end are clamped onto the last valid row: their products
+    // land in accumulator rows the epilogue never stores, and the loads stay
+    // unconditional, which keeps the compiler's vmcnt tracking exact (a
+    // branch around a load makes it wait for every load in flight).
+    const bf16_t* wsrc[CW];
+    const bf16_t* xsrc[CX];
+#pragma unroll
+    for (int i = 0; i < CW; ++i) {
+        int c = tid + NT * i, row = c >> 3, kc = c & 7;
+        int f = min(f0 + row, a.n - 1);
+        wsrc[i] = a.w + (long)f * a.k + kc * 8;
+    }
+#pragma unroll
+    for (int i = 0; i < CX; ++i) {
+        int c = tid + NT * i, row = c >> 3, kc = c & 7;
+        int t = min(t0 + row, a.rows - 1);
+        long src = a.gather ? (long)a.gather[t] : (long)t;
+        xsrc[i] = a.x + src * a.ldx + kc * 8;
+    }
+
+    struct Stage {
+        u32x4 w[CW], x[CX];
+    };
+    auto gload = [&](Stage& s, int kt) {
+        const int kb = kt * BK;
+#pragma unroll
+        for (int i = 0; i < CW; ++i) s.w[i] = *(const u32x4*)(wsrc[i] + kb);
+#pragma unroll
+        for (int i = 0; i < CX; ++i) s.x[i] = *(const u32x4*)(xsrc[i] + kb);
+    };
+    auto sstore = [&](const Stage& s, int buf) {
+#pragma unroll
+        for (int i = 0; i < CW; ++i) {
+            int c = tid + NT * i;
+            *(u32x4*)&sW[buf][c >> 3][(c & 7) * 8] = s.w[i];
+        }
+#pragma unroll
+        for (int i = 0; i < CX; ++i) {
+            int c = tid + NT * i;
+            *(u32x4*)&sX[buf][c >> 3][(c & 7) * 8] = s.x[i];
+        }
+    };
+
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wf = wave % WF, wt = wave / WF;
+    const int lr = lane & 31, lk = (lane >> 5) * 8;
+
+    f32x16 acc[FB][TB];
+#pragma unroll
+    for (int i = 0; i < FB; ++i)
+#pragma unroll
+        for (int j = 0; j < TB; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+    auto compute = [&](int buf) {
+#pragma unroll
+        for (int ks = 0; ks < BK / 16; ++ks) {
+            bf16x8 af[FB], bx[TB];
+#pragma unroll
+            for (int i = 0; i < FB; ++i) af[i] = *(const bf16x8*)&sW[buf][wf * FPW + i * 32 + lr][ks * 16 + lk];
+#pragma unroll
+            for (int j = 0; j < TB; ++j) bx[j] = *(const bf16x8*)&sX[buf][wt * TPW + j * 32 + lr][ks * 16 + lk];
+#pragma unroll
+            for (int i = 0; i < FB; ++i)
+#pragma unroll
+                for (int j = 0; j < TB; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bx[j], acc[i][j], 0, 0, 0);
+        }
+    };
+
+    // K steps kt = 0..KT-1.  Tile kt is loaded into register stage kt%2 two
+    // steps ahead and stored to LDS buffer kt%2 at the end of step kt-1.  The
+    // prefetch index is clamped instead of skipped near the end (re-reading the
+    // last tile from L2) so the steady-state loop carries no branches.
+    const int KT = a.k / BK;
+    Stage r0, r1;
+    gload(r0, 0);
+    gload(r1, min(1, KT - 1));
+    sstore(r0, 0);
+    __syncthreads();
+    gload(r0, min(2, KT - 1));
+    // One step: compute from LDS buf; stage `nxt` holds tile kt+1 -> LDS buf^1;
+    // then refill `nxt` with tile kt+3.
+    auto step = [&](int kt, Stage& nxt) {
+        const int buf = kt & 1;
+        compute(buf);
+        sstore(nxt, buf ^ 1);
+        gload(nxt, min(kt + 3, KT - 1));
+        __syncthreads();
+    };
+    int kt = 0;
+    for (; kt + 1 < KT; kt += 2) {
+        step(kt, r1);
+        step(kt + 1, r0);
+    }
+    if (kt < KT) compute(kt & 1);
+
+    epilogue<EPI, FB, TB>(a, acc, f0 + wf * FPW, t0 + wt * TPW, lane);
+}
+
+// Tile shape: 128 features x 128 tokens, four waves of 64x64, two resident
+// workgroups per CU (73.7 KB of LDS each).  Measured on MI355X against
+// 256x256 (8 waves of 128x64, one workgroup per CU) and 256x128 (4 waves of
+// 128x64): the two independent workgroups per CU hide each other's barrier
+// and LDS latency, which outweighs the 25-50% fewer LDS bytes per MFMA of the
+// wider wave tiles at one workgroup per CU.
 template <int EPI>
 void launch_cfg(const GemmArgs& a, hipStream_t s) {
-    constexpr int BF = 128, BT = 128, WF = 2, WT = 2;
-    int nF = (a.n + BF - 1) / BF, nTk = (a.rows + BT - 1) / BT;
-    int blocks = nF * nTk;
-    hipLaunchKernelGGL((gemm_kernel<EPI, BF, BT, WF, WT>), dim3(blocks), dim3(WF * WT * 64), 0, s, a);
+    constexpr int BF = 128, BT = 128;
+    const int blocks = ((a.n + BF - 1) / BF) * ((a.rows + BT - 1) / BT);
+    hipLaunchKernelGGL((gemm_kernel<EPI, BF, BT, 2, 2>), dim3(blocks), dim3(256), 0, s, a);
     HIP_CHECK(hipGetLastError());
 }
 
