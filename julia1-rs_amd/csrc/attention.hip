@@ -100,8 +100,13 @@ __global__ __launch_bounds__(NTHR) void attention_kernel(AttnArgs a) {
     f32x16 o[2];
 #pragma unroll
     for (int e = 0; e < 16; ++e) o[0][e] = o[1][e] = 0.0f;
+    // Online softmax in log2 units: p = exp2(c·s - c·m) with c = scale·log2(e),
+    // evaluated as one FMA per score; m is the running max of the raw scores.
     float m = -INFINITY, l = 0.0f;
-    const float sl2 = a.scale_log2;
+    const float c = a.scale_log2;
+    // Queries of this wave sit at positions [qlo, qlo + 31].
+    const int qlo = tile.q_pos + wave * 32;
+    const unsigned w2 = 2u * (unsigned)a.window;
 
     const int ntk = kend > kbeg ? (kend - kbeg + KT - 1) / KT : 0;
     if (ntk > 0) {
@@ -125,38 +130,53 @@ __global__ __launch_bounds__(NTHR) void attention_kernel(AttnArgs a) {
                 s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], s[kb], 0, 0, 0);
             }
         }
-        // Mask + scale; element e of block kb is key k0 + kb*32 + (e/4)*8 + 4g + e%4.
+        // Masking only where this wave's (query, key) block can hold an invalid
+        // pair (decided per wave, so the branch is uniform): the sequence end,
+        // or a sliding window edge.  Element e of block kb is key
+        // k0 + kb*32 + (e/4)*8 + 4g + e%4.
+        const bool tail = k0 + KT > kend;
+        const bool edge = a.window >= 0 && (k0 < qlo + 31 - a.window || k0 + KT - 1 > qlo + a.window);
+        if (tail || edge) {
+            const int kl = k0 + 4 * g;     // key of element 0 in block 0 for this lane
+            const int dq = qpos - kl;      // query - key for element 0
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int off = kb * 32 + (e >> 2) * 8 + (e & 3);
+                    bool ok = kl + off < kend;
+                    if (a.window >= 0) ok = ok && (unsigned)(dq - off + a.window) <= w2;
+                    s[kb][e] = ok ? s[kb][e] : -INFINITY;
+                }
+        }
         float mx = -INFINITY;
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                int key = k0 + kb * 32 + (e >> 2) * 8 + g * 4 + (e & 3);
-                bool ok = key < kend && (a.window < 0 || abs(qpos - key) <= a.window);
-                float v = ok ? s[kb][e] * sl2 : -INFINITY;
-                s[kb][e] = v;
-                mx = fmaxf(mx, v);
-            }
+            for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[kb][e]);
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
         const float mn = fmaxf(m, mx);
-        const float u = mn == -INFINITY ? 0.0f : mn;
-        const float alpha = __builtin_amdgcn_exp2f(m - u);
-        m = mn;
+        if (__any(mn > m)) {  // rescale only when some running max moved
+            const float alpha = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m - mn) * c);
+            l *= alpha;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                o[0][e] *= alpha;
+                o[1][e] *= alpha;
+            }
+            m = mn;
+        }
+        const float mc = m == -INFINITY ? 0.0f : m * c;
         float ls = 0.0f;
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
-                float p = __builtin_amdgcn_exp2f(s[kb][e] - u);
+                float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][e], c, -mc));
                 s[kb][e] = p;
                 ls += p;
             }
-        l = l * alpha + ls;
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            o[0][e] *= alpha;
-            o[1][e] *= alpha;
-        }
+        l += ls;
         // Oᵀ += Vᵀ·Pᵀ over 4 steps of 16 keys.  Step (kb, hb) uses accumulator
         // elements hb*8 .. hb*8+7 of block kb: keys base + 8*(e/4) + 4g + e%4.
 #pragma unroll

@@ -87,7 +87,7 @@ DevBuf upload_f32(const float* src, size_t n) {
 DevBuf upload_bf16(const float* src, size_t n) {
     if (!src) throw jh_error(JH_ERR_INVALID, "missing weight tensor");
     std::vector<bf16_t> tmp(n);
-    for (size_t i = 0; i < n; ++i) tmp[i] = f2bf(src[i]);
+    for (size_t i = 0; i < n; ++i) tmp[i] = f2bf_host(src[i]);
     return upload_bytes(tmp.data(), n * sizeof(bf16_t));
 }
 

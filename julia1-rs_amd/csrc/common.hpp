@@ -16,6 +16,8 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 #define JH_WAVE 64
 
@@ -32,18 +34,25 @@ struct jh_error : std::runtime_error {
             throw jh_error(2, std::string(#call) + ": " + hipGetErrorString(e_));                    \
     } while (0)
 
-// float -> bf16 bits, round to nearest even, NaN kept quiet (as half::bf16::from_f32).
-__host__ __device__ inline bf16_t f2bf(float f) {
-    uint32_t u = __builtin_bit_cast(uint32_t, f);
+// float -> bf16 bits on the host, round to nearest even, NaN kept quiet
+// (as half::bf16::from_f32, used for the one-time weight conversion).
+inline bf16_t f2bf_host(float f) {
+    uint32_t u;
+    __builtin_memcpy(&u, &f, 4);
     if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16_t)((u >> 16) | 0x40);
     u += 0x7fffu + ((u >> 16) & 1u);
     return (bf16_t)(u >> 16);
 }
 
+// Device conversions use gfx950's v_cvt_pk_bf16_f32 (round to nearest even).
+__device__ inline bf16_t f2bf(float f) { return __builtin_bit_cast(bf16_t, (__bf16)f); }
+
 __host__ __device__ inline float bf2f(bf16_t b) { return __builtin_bit_cast(float, (uint32_t)b << 16); }
 
-// Two floats -> packed bf16x2 (low half = a), RNE.
-__device__ inline uint32_t pack2(float a, float b) { return (uint32_t)f2bf(a) | ((uint32_t)f2bf(b) << 16); }
+// Two floats -> packed bf16x2 (low half = a), one v_cvt_pk_bf16_f32.
+__device__ inline uint32_t pack2(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
+}
 
 __device__ inline float wave_sum(float v) {
 #pragma unroll
