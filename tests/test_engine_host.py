@@ -1,0 +1,124 @@
+"""C++ host engine (include/julia1_engine.h) checks that need no GPU: device
+strings (src/engine.rs:20-32), the checkpoint reader's config/safetensors/
+tensor-resolution paths and their error messages (src/config.rs:43-96,
+src/weights.rs:51-89, src/model.rs:55-110, src/engine.rs:89-172)."""
+import json
+import os
+import struct
+
+import numpy as np
+import pytest
+
+from julia1_amd import engine, hip, synth
+
+
+@pytest.fixture(scope="module")
+def tiny_ckpt(tmp_path_factory):
+    root = str(tmp_path_factory.mktemp("tiny"))
+    cfg = synth.model_config("tiny")
+    synth.write_checkpoint(root, "tiny", synth.make_weights(cfg, seed=1))
+    return root
+
+
+def test_parse_device():
+    assert engine.parse_device("hip") == 0
+    assert engine.parse_device("hip:3") == 3
+    for bad in ("cpu", "cuda", "cuda:0", "hip:", "hip:x", "hip:-1", ""):
+        with pytest.raises(hip.HipError, match="device must be hip or hip:N"):
+            engine.parse_device(bad)
+
+
+def test_inspect_reads_whole_checkpoint(tiny_ckpt):
+    s = engine.inspect(tiny_ckpt)
+    cfg = synth.model_config("tiny")
+    assert s["hidden"] == 128 and s["layers"] == 3 and s["head_layers"] == 2
+    assert s["tensors"] == len(synth.tensor_specs(cfg))
+    assert s["bytes"] == os.path.getsize(os.path.join(tiny_ckpt, "model.safetensors"))
+
+
+def _copy_ckpt(src, dst, julia=None, enc=None, weights=None):
+    os.makedirs(os.path.join(dst, "encoder"), exist_ok=True)
+    j = json.load(open(os.path.join(src, "julia_config.json")))
+    e = json.load(open(os.path.join(src, "encoder", "config.json")))
+    j.update(julia or {})
+    e.update(enc or {})
+    json.dump(j, open(os.path.join(dst, "julia_config.json"), "w"))
+    json.dump(e, open(os.path.join(dst, "encoder", "config.json"), "w"))
+    if weights is None:
+        os.symlink(os.path.join(src, "model.safetensors"), os.path.join(dst, "model.safetensors"))
+    else:
+        open(os.path.join(dst, "model.safetensors"), "wb").write(weights)
+    return dst
+
+
+@pytest.mark.parametrize("julia,enc,msg", [
+    ({"format_version": 2}, {}, "Unsupported Julia checkpoint format"),
+    ({"weight_dtype": "int8"}, {}, "Only float32 Julia checkpoints are supported"),
+    ({}, {"model_type": "bert"}, "Encoder must be ModernBERT"),
+    ({}, {"norm_bias": True}, "Unsupported encoder setting norm_bias"),
+    ({}, {"hidden_activation": "relu"}, "Unsupported encoder activation"),
+    ({}, {"num_attention_heads": 4}, "Runtime kernels require head_dim 64"),
+    ({}, {"layer_types": ["full_attention"]}, "layer_types must list every layer"),
+    ({}, {"rope_parameters": {"full_attention": {"rope_type": "yarn", "rope_theta": 1.0}}}, "Only default RoPE"),
+    ({"head_layers": None}, {}, "config is missing head_layers"),
+])
+def test_config_errors(tiny_ckpt, tmp_path, julia, enc, msg):
+    d = _copy_ckpt(tiny_ckpt, str(tmp_path / "c"), julia, enc)
+    with pytest.raises(hip.HipError, match=msg):
+        engine.inspect(d)
+
+
+def _safetensors(tensors, dtype="F32"):
+    header, blobs, off = {}, [], 0
+    for name, a in tensors.items():
+        b = a.astype(np.float32 if dtype == "F32" else np.float16).tobytes()
+        header[name] = {"dtype": dtype, "shape": list(a.shape), "data_offsets": [off, off + len(b)]}
+        blobs.append(b)
+        off += len(b)
+    h = json.dumps(header).encode()
+    return struct.pack("<Q", len(h)) + h + b"".join(blobs)
+
+
+def test_safetensors_errors(tiny_ckpt, tmp_path):
+    cases = [
+        (b"version https://git-lfs.github.com/spec/v1\noid sha256:00\nsize 1\n", "Git LFS pointers"),
+        (b"\x01\x02", "Truncated safetensors file"),
+        (struct.pack("<Q", 1 << 40) + b"{}", "Truncated safetensors header"),
+        (_safetensors({"x": np.zeros(3)}, dtype="F16"), "only F32 tensors are supported"),
+        (_safetensors({"x": np.zeros(3)}), "missing tensor encoder.embeddings.tok_embeddings.weight"),
+    ]
+    for i, (blob, msg) in enumerate(cases):
+        d = _copy_ckpt(tiny_ckpt, str(tmp_path / f"s{i}"), weights=blob)
+        with pytest.raises(hip.HipError, match=msg):
+            engine.inspect(d)
+
+
+def test_wrong_tensor_shape(tmp_path):
+    cfg = synth.model_config("tiny")
+    t = synth.make_weights(cfg, seed=2)
+    t["encoder.layers.1.mlp.Wo.weight"] = np.zeros((128, 100), dtype=np.float32)
+    d = synth.write_checkpoint(str(tmp_path / "w"), "tiny", t)
+    with pytest.raises(hip.HipError, match=r"encoder.layers.1.mlp.Wo.weight: expected shape \[128, 192\], found \[128, 100\]"):
+        engine.inspect(d)
+
+
+def test_load_option_errors_before_any_device(tiny_ckpt, tmp_path):
+    with pytest.raises(hip.HipError, match="max_length must be an integer between 1 and 256"):
+        engine.Engine.load(tiny_ckpt, max_length=257)
+    with pytest.raises(hip.HipError, match="Invalid batch size / token budget"):
+        engine.Engine.load(tiny_ckpt, batch_size=0)
+    with pytest.raises(hip.HipError, match="Invalid batch size / token budget"):
+        engine.Engine.load(tiny_ckpt, max_batch_tokens=100)
+    d = _copy_ckpt(tiny_ckpt, str(tmp_path / "q"))
+    open(os.path.join(d, "quantization.json"), "w").write("{}")
+    with pytest.raises(hip.HipError, match="INT8 checkpoints are not supported"):
+        engine.Engine.load(d)
+
+
+def test_load_without_gpu_fails_cleanly(tiny_ckpt):
+    torch = pytest.importorskip("torch")
+    if torch.cuda.device_count() > 0:
+        pytest.skip("a GPU is present; covered by the GPU tests")
+    with pytest.raises(hip.HipError) as e:
+        engine.Engine.load(tiny_ckpt)
+    assert e.value.code == 2

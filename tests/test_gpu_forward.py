@@ -146,3 +146,51 @@ def test_invalid_batches_rejected(tiny):
     # the model still works after rejected calls
     s = parity(b, gpu.forward(b), tiny[2].forward(b))
     check_gates(s)
+
+
+def test_hidden_384_shape():
+    """The reference CUDA path's own hidden size (src/cuda/mod.rs:175) through the same kernels."""
+    cfg = synth.model_config("julia1-384")
+    ws = abi.WeightSet(cfg, synth.make_weights(cfg, seed=5))
+    gpu, orc = hip.HipModel(ws), oracle.OracleModel(ws)
+    b = synth.make_batch([300, 64, 129, 7], [5, 3, 20, 2], cfg.vocab, 17)
+    s = parity(b, gpu.forward(b), orc.forward(b))
+    print("h384", s)
+    check_gates(s)
+
+
+def test_base_config4_slice(base):
+    """32 rows of the router-scale varlen batch against the oracle."""
+    ws, gpu, orc = base
+    b = synth.workload("config4").subset(range(0, 256, 8))
+    s = parity(b, gpu.forward(b), orc.forward(b))
+    print("config4[::8]", s)
+    check_gates(s)
+
+
+def test_base_config4_full_size_properties(base):
+    """Full ~135k-token config4: permutation invariance across the whole batch,
+    finite outputs, and sampled rows against the oracle."""
+    ws, gpu, orc = base
+    b = synth.workload("config4")
+    got = b.split_scores(gpu.forward(b))
+    assert all(np.all(np.isfinite(g)) for g in got)
+    perm = np.random.default_rng(0).permutation(b.lens.size)
+    pb = b.subset(perm)
+    pgot = pb.split_scores(gpu.forward(pb))
+    for k, i in enumerate(perm):
+        assert np.abs(pgot[k] - got[i]).max() <= 1e-4
+    rows = [3, 77, 200, 255]
+    sb = b.subset(rows)
+    ref = sb.split_scores(orc.forward(sb))
+    for k, i in enumerate(rows):
+        assert np.abs(got[i] - ref[k]).max() <= 2e-2
+
+
+def test_base_long_sequence_8192(base):
+    """One full-length 8192-token row of configs[3] against the oracle."""
+    ws, gpu, orc = base
+    b = synth.workload("config3").subset([0])
+    s = parity(b, gpu.forward(b), orc.forward(b))
+    print("config3[0]", s)
+    check_gates(s)
