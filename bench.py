@@ -54,6 +54,22 @@ def roofline(stat):
                 launch_us=round(per_launch_ms * 1e3, 2), bytes_per_launch=stat["bytes"] / stat["launches"])
 
 
+def committed_traffic(kernel, workload, roof):
+    """HBM bytes per launch of `kernel` on `workload` from profiles/traffic.md (rocprofv3
+    FETCH_SIZE + WRITE_SIZE per dispatch, calibrated on a plain copy), or None."""
+    path = os.path.join(ROOT, "profiles", "traffic.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) >= 5 and cells[0] == kernel and cells[1] == workload:
+            try:
+                return int(float(cells[4]))
+            except ValueError:
+                return None
+    return None
+
+
 def kernel_table(stats, steps):
     out = []
     for s in sorted(stats, key=lambda s: -s["ms"]):
@@ -76,6 +92,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip the GEMM sweep and the L=8192 attention run")
     ap.add_argument("--cpu-threads", type=int, default=None)
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="also run 3 device-to-device copies of MIB MiB (the known-size kernel that "
+                         "calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -131,6 +150,16 @@ def main():
     gemm_flops = sum(s["flops"] for s in stats if s["name"] in ENCODER_GEMMS)
     gemm_util = gemm_flops / (gemm_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS * 100
     prof_step_ms = sum(s["ms"] for s in stats) / args.steps
+
+    if args.copy_probe:
+        src = torch.empty(args.copy_probe << 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
+    roof["traffic"] = committed_traffic(roof["kernel"], args.workload, roof)
 
     extra = {}
     if not args.no_extra:

@@ -229,6 +229,6 @@ void launch_attention(const AttnArgs& a, hipStream_t s) {
         ((uintptr_t)a.q & 15) || ((uintptr_t)a.k & 15) || ((uintptr_t)a.v & 15) || ((uintptr_t)a.out & 7))
         throw jh_error(1, "attention: operands must be 16-byte aligned with row strides % 8 == 0");
     if (a.ntiles > 0x7fffffff || a.heads > 65535) throw jh_error(1, "attention: grid too large");
-    hipLaunchKernelGGL(attention_kernel, dim3(a.ntiles, a.heads), dim3(NTHR), 0, s, a);
+    JH_LAUNCH(attention_kernel, dim3(a.ntiles, a.heads), dim3(NTHR), 0, s, a);
     HIP_CHECK(hipGetLastError());
 }

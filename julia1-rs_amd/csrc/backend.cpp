@@ -164,7 +164,7 @@ struct jh_model {
     std::string name;
     // attention (query, key) pairs of the staged batch, for algorithmic FLOPs
     double pairs_global = 0, pairs_local = 0, pairs_marker = 0;
-    // profiling: one event pair per launch while enabled
+    // profiling: one event pair per launch, stamped at the dispatch, while enabled
     bool profiling = false;
     std::vector<hipEvent_t> ev_pool;
     size_t ev_next = 0;
@@ -192,9 +192,15 @@ struct jh_model {
             return;
         }
         ProfRec r{cls, flops, bytes, next_event(), next_event()};
-        HIP_CHECK(hipEventRecord(r.a, stream));
-        launch();
-        HIP_CHECK(hipEventRecord(r.b, stream));
+        const LaunchEvents ev{r.a, r.b};
+        jh_launch_events = &ev;
+        try {
+            launch();
+        } catch (...) {
+            jh_launch_events = nullptr;
+            throw;
+        }
+        jh_launch_events = nullptr;
         recs.push_back(r);
     }
 

@@ -268,7 +268,7 @@ template <int EPI>
 void launch_cfg(const GemmArgs& a, hipStream_t s) {
     constexpr int BF = 128, BT = 128;
     const int blocks = ((a.n + BF - 1) / BF) * ((a.rows + BT - 1) / BT);
-    hipLaunchKernelGGL((gemm_kernel<EPI, BF, BT, 2, 2>), dim3(blocks), dim3(256), 0, s, a);
+    JH_LAUNCH((gemm_kernel<EPI, BF, BT, 2, 2>), dim3(blocks), dim3(256), 0, s, a);
     HIP_CHECK(hipGetLastError());
 }
 

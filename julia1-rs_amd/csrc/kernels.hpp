@@ -3,7 +3,27 @@
 // before launching anything that could read or write out of bounds.
 #pragma once
 
+#include <hip/hip_ext.h>
+
 #include "common.hpp"
+
+// Profiling hook: when a launch wrapper runs with a non-null jh_launch_events,
+// its kernel is dispatched with hipExtLaunchKernelGGL so the runtime stamps
+// the start/stop events at the dispatch itself (the same interval rocprofv3
+// reports), instead of separate event packets around it.
+struct LaunchEvents {
+    hipEvent_t start, stop;
+};
+inline thread_local const LaunchEvents* jh_launch_events = nullptr;
+
+#define JH_LAUNCH(kernel, grid, block, shm, stream, ...)                                                          \
+    do {                                                                                                          \
+        if (jh_launch_events)                                                                                     \
+            hipExtLaunchKernelGGL(kernel, grid, block, shm, stream, jh_launch_events->start,                      \
+                                  jh_launch_events->stop, 0, __VA_ARGS__);                                        \
+        else                                                                                                      \
+            hipLaunchKernelGGL(kernel, grid, block, shm, stream, __VA_ARGS__);                                    \
+    } while (0)
 
 struct GemmArgs {
     const bf16_t* x;        // activations, row stride ldx (elements)

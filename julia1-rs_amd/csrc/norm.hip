@@ -196,7 +196,7 @@ void launch_embed_ln(const uint32_t* ids, int rows, const float* table, const fl
                      float* x, bf16_t* xn, hipStream_t s) {
     if (rows <= 0) return;
     dispatch_hidden(hidden, [&]<int EPL>() {
-        hipLaunchKernelGGL(embed_ln_kernel<EPL>, row_grid(rows), dim3(256), 0, s, ids, rows, table, w, eps, x, xn);
+        JH_LAUNCH(embed_ln_kernel<EPL>, row_grid(rows), dim3(256), 0, s, ids, rows, table, w, eps, x, xn);
     });
     HIP_CHECK(hipGetLastError());
 }
@@ -205,7 +205,7 @@ void launch_layer_norm(const float* x, int rows, const float* w, const float* b,
                        hipStream_t s) {
     if (rows <= 0) return;
     dispatch_hidden(hidden, [&]<int EPL>() {
-        hipLaunchKernelGGL(layer_norm_kernel<EPL>, row_grid(rows), dim3(256), 0, s, x, rows, w, b, eps, out);
+        JH_LAUNCH(layer_norm_kernel<EPL>, row_grid(rows), dim3(256), 0, s, x, rows, w, b, eps, out);
     });
     HIP_CHECK(hipGetLastError());
 }
@@ -214,7 +214,7 @@ void launch_final_norm(float* x, int rows, const float* fw, const float* type_em
                        const float* hw, const float* hb, float eps, int hidden, bf16_t* out, hipStream_t s) {
     if (rows <= 0) return;
     dispatch_hidden(hidden, [&]<int EPL>() {
-        hipLaunchKernelGGL(final_norm_kernel<EPL>, row_grid(rows), dim3(256), 0, s, x, rows, fw, type_emb, tok_meta,
+        JH_LAUNCH(final_norm_kernel<EPL>, row_grid(rows), dim3(256), 0, s, x, rows, fw, type_emb, tok_meta,
                            hw, hb, eps, out);
     });
     HIP_CHECK(hipGetLastError());
@@ -223,7 +223,7 @@ void launch_final_norm(float* x, int rows, const float* fw, const float* type_em
 void launch_gather_f32(const float* src, const int32_t* idx, int rows, int hidden, float* dst, hipStream_t s) {
     if (rows <= 0) return;
     dispatch_hidden(hidden, [&]<int EPL>() {
-        hipLaunchKernelGGL(gather_kernel<EPL>, row_grid(rows), dim3(256), 0, s, src, idx, rows, dst);
+        JH_LAUNCH(gather_kernel<EPL>, row_grid(rows), dim3(256), 0, s, src, idx, rows, dst);
     });
     HIP_CHECK(hipGetLastError());
 }
@@ -231,7 +231,7 @@ void launch_gather_f32(const float* src, const int32_t* idx, int rows, int hidde
 void launch_scorer(const float* z, int rows, int hidden, const float* w2, float b2, float* out, hipStream_t s) {
     if (rows <= 0) return;
     dispatch_hidden(hidden, [&]<int EPL>() {
-        hipLaunchKernelGGL(scorer_kernel<EPL>, row_grid(rows), dim3(256), 0, s, z, rows, w2, b2, out);
+        JH_LAUNCH(scorer_kernel<EPL>, row_grid(rows), dim3(256), 0, s, z, rows, w2, b2, out);
     });
     HIP_CHECK(hipGetLastError());
 }
