@@ -43,7 +43,8 @@ enum {
  *  bias f32 [N] (NULL allowed for RESID_F32).
  *  ROPE: pos[r] is the row's position; cos/sin are [positions, 32] f32 tables;
  *        columns < rope_cols are rotated per 64-wide head.
- * Requirements: K % 64 == 0, N % 64 == 0, K <= 8192.  Replaces cuBLAS gemm_ex
+ * Requirements: K % 64 == 0, N % 64 == 0, K <= 8192; x, w and out 16-byte aligned,
+ * and out's rows and column `col` on 16-byte boundaries.  Replaces cuBLAS gemm_ex
  * (src/cuda/mod.rs:347-375) plus the separate geglu/bias_act kernels
  * (src/cuda/kernels.cu:137-172) and the residual add of ln_bf16 (:97-109).
  */

@@ -8,13 +8,10 @@
 // what the epilogues want: 16-byte FP32 residual read-modify-writes, and the
 // RoPE pair (d, d+32) and the GEGLU pair (gate, up) in the same lane.
 //
-// Pipeline: workgroup tile BF features x BT tokens x BK=64.  Global loads run
-// two K steps ahead of the MFMAs (two register stages), LDS is double
-// buffered, one barrier per K step.  At K = 768 that keeps 2/12 of the whole
-// operand stream in flight per workgroup, which hides the HBM/MALL latency.
-// All loads are unconditional (out-of-range rows are clamped) so the
-// compiler's vmcnt waits stay exact.  LDS rows are padded to 72 bf16 (144 B)
-// so the 16-byte fragment reads of 8 consecutive rows hit distinct banks.
+// Pipeline: workgroup tile 128 features x 128 tokens x BK=64, four waves of
+// 64x64.  Operands go global -> LDS by DMA (no register staging, 47 VGPRs),
+// double-buffered: the DMA of K step kt+1 runs under the MFMAs of step kt,
+// one barrier per step, two resident workgroups per CU (64 KB LDS each).
 //
 // Tiles are dealt XCD-contiguously: MI355X hands workgroups round-robin to its
 // 8 XCDs, so tile t goes to the workgroup whose id mod 8 selects the XCD that
@@ -28,123 +25,155 @@
 namespace {
 
 constexpr int BK = 64;
-constexpr int LDS_STRIDE = 72;
 
-template <int EPI, int FB, int TB>
-__device__ inline void epilogue(const GemmArgs& a, f32x16 (&acc)[FB][TB], int fw0, int tw0, int lane) {
-    // acc[i][j][e]: feature fw0 + i*32 + (e/4)*8 + g4 + e%4, token tw0 + j*32 + lr.
+// LDS chunk swizzle of operand row r (see gemm_kernel).
+__device__ constexpr int swz(int r) { return (r >> 1) & 7; }
+
+// Staging-row swizzle for rows of CPR 16-byte chunks: the 16 rows that a
+// quarter-wave writes (one chunk each) land on 16 distinct 16-byte bank slots.
+template <int CPR>
+__device__ constexpr int oswz(int r) {
+    return CPR == 16 ? (r & 15) : ((r >> 1) & 7);
+}
+
+// Epilogue of one wave's 64 x 64 tile (features fw0.., tokens tw0..).
+// acc[i][j][e] holds feature fw0 + i*32 + (e/4)*8 + g4 + e%4 of token
+// tw0 + j*32 + lr.  Phase 1 applies the elementwise part in registers and
+// writes FP32 results to the wave's staging rows in LDS ([token][column]);
+// phase 2 reads them back along rows so each store instruction writes whole
+// 128/256-byte row segments (8 or 4 rows per instruction) instead of 32
+// scattered 16-byte pieces.
+template <int EPI>
+__device__ inline void epilogue(const GemmArgs& a, f32x16 (&acc)[2][2], int fw0, int tw0, int lane, float* stage) {
+    constexpr bool GEGLU = EPI == JH_EPI_GEGLU_BF16;
+    constexpr bool F32OUT = EPI == JH_EPI_RESID_F32 || EPI == JH_EPI_BIAS_F32;
+    constexpr int OW = GEGLU ? 32 : 64;  // output columns of the wave tile
+    constexpr int CPR = OW / 4;          // 16-byte FP32 chunks per staging row
     const int g4 = (lane >> 5) * 4, lr = lane & 31;
+    auto put = [&](int row, int chunk, f32x4 v) { *(f32x4*)&stage[row * OW + ((chunk ^ oswz<CPR>(row)) * 4)] = v; };
+
 #pragma unroll
-    for (int j = 0; j < TB; ++j) {
-        const int t = tw0 + j * 32 + lr;
-        if (t >= a.rows) continue;
-        if constexpr (EPI == JH_EPI_ROPE_BF16 || EPI == JH_EPI_GEGLU_BF16) {
+    for (int j = 0; j < 2; ++j) {
+        const int tl = j * 32 + lr;
+        if constexpr (EPI == JH_EPI_ROPE_BF16) {
+            const bool rot = fw0 < a.rope_cols;
+            const long p = rot ? (long)(a.pos[min(tw0 + tl, a.rows - 1)] & 0xffff) * 32 : 0;
 #pragma unroll
-            for (int i = 0; i < FB; i += 2) {
-                const int slab = fw0 + i * 32;  // 64-aligned: [slab, slab+32) pairs with [slab+32, slab+64)
-                if (slab >= a.n) continue;
-                if constexpr (EPI == JH_EPI_ROPE_BF16) {
-                    bf16_t* o = (bf16_t*)a.out + (long)t * a.ldo + a.col + slab;
-                    const bool rot = slab < a.rope_cols;
-                    const long p = rot ? (long)(a.pos[t] & 0xffff) * 32 : 0;
+            for (int qd = 0; qd < 4; ++qd) {
+                const int d = qd * 8 + g4;
+                f32x4 lo, hi;
 #pragma unroll
-                    for (int qd = 0; qd < 4; ++qd) {
-                        const int d = qd * 8 + g4;
-                        float lo[4], hi[4];
+                for (int e = 0; e < 4; ++e) {
+                    lo[e] = acc[0][j][qd * 4 + e];
+                    hi[e] = acc[1][j][qd * 4 + e];
+                }
+                if (rot) {
+                    const f32x4 c = *(const f32x4*)(a.cos_t + p + d);
+                    const f32x4 s = *(const f32x4*)(a.sin_t + p + d);
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            lo[e] = acc[i][j][qd * 4 + e];
-                            hi[e] = acc[i + 1][j][qd * 4 + e];
-                        }
-                        if (rot) {
-                            f32x4 c = *(const f32x4*)(a.cos_t + p + d);
-                            f32x4 s = *(const f32x4*)(a.sin_t + p + d);
-#pragma unroll
-                            for (int e = 0; e < 4; ++e) {
-                                float x0 = lo[e], x1 = hi[e];
-                                lo[e] = x0 * c[e] - x1 * s[e];
-                                hi[e] = x1 * c[e] + x0 * s[e];
-                            }
-                        }
-                        *(u32x2*)(o + d) = u32x2{pack2(lo[0], lo[1]), pack2(lo[2], lo[3])};
-                        *(u32x2*)(o + 32 + d) = u32x2{pack2(hi[0], hi[1]), pack2(hi[2], hi[3])};
-                    }
-                } else {
-                    bf16_t* o = (bf16_t*)a.out + (long)t * a.ldo + a.col + slab / 2;
-#pragma unroll
-                    for (int qd = 0; qd < 4; ++qd) {
-                        const int d = qd * 8 + g4;
-                        float g[4];
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) g[e] = gelu_erf(acc[i][j][qd * 4 + e]) * acc[i + 1][j][qd * 4 + e];
-                        *(u32x2*)(o + d) = u32x2{pack2(g[0], g[1]), pack2(g[2], g[3])};
+                    for (int e = 0; e < 4; ++e) {
+                        const float x0 = lo[e], x1 = hi[e];
+                        lo[e] = x0 * c[e] - x1 * s[e];
+                        hi[e] = x1 * c[e] + x0 * s[e];
                     }
                 }
+                put(tl, d / 4, lo);
+                put(tl, 8 + d / 4, hi);
+            }
+        } else if constexpr (GEGLU) {
+            // Rows [fw0, fw0+32) are gate, [fw0+32, fw0+64) up, for outputs fw0/2 + [0, 32).
+#pragma unroll
+            for (int qd = 0; qd < 4; ++qd) {
+                const int d = qd * 8 + g4;
+                f32x4 g;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) g[e] = gelu_erf(acc[0][j][qd * 4 + e]) * acc[1][j][qd * 4 + e];
+                put(tl, d / 4, g);
             }
         } else {
 #pragma unroll
-            for (int i = 0; i < FB; ++i) {
-                const int slab = fw0 + i * 32;
-                if (slab >= a.n) continue;
+            for (int i = 0; i < 2; ++i)
 #pragma unroll
                 for (int qd = 0; qd < 4; ++qd) {
-                    const int f = slab + qd * 8 + g4;
-                    float v[4];
+                    const int fl = i * 32 + qd * 8 + g4;
+                    f32x4 v;
 #pragma unroll
                     for (int e = 0; e < 4; ++e) v[e] = acc[i][j][qd * 4 + e];
-                    if constexpr (EPI == JH_EPI_STORE_BF16) {
-                        bf16_t* o = (bf16_t*)a.out + (long)t * a.ldo + a.col + f;
-                        *(u32x2*)o = u32x2{pack2(v[0], v[1]), pack2(v[2], v[3])};
-                    } else if constexpr (EPI == JH_EPI_RESID_F32) {
-                        float* o = (float*)a.out + (long)t * a.ldo + a.col + f;
-                        f32x4 old = *(const f32x4*)o;
-                        if (a.bias) {
-                            f32x4 bb = *(const f32x4*)(a.bias + f);
-#pragma unroll
-                            for (int e = 0; e < 4; ++e) old[e] += v[e] + bb[e];
-                        } else {
-#pragma unroll
-                            for (int e = 0; e < 4; ++e) old[e] += v[e];
-                        }
-                        *(f32x4*)o = old;
-                    } else {
-                        f32x4 bb = *(const f32x4*)(a.bias + f);
+                    if (EPI != JH_EPI_STORE_BF16 && (EPI != JH_EPI_RESID_F32 || a.bias)) {
+                        const f32x4 bb = *(const f32x4*)(a.bias + fw0 + fl);
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
                             v[e] += bb[e];
                             if constexpr (EPI == JH_EPI_BIAS_RELU_BF16) v[e] = fmaxf(v[e], 0.0f);
                         }
-                        if constexpr (EPI == JH_EPI_BIAS_F32) {
-                            *(f32x4*)((float*)a.out + (long)t * a.ldo + a.col + f) = f32x4{v[0], v[1], v[2], v[3]};
-                        } else {
-                            bf16_t* o = (bf16_t*)a.out + (long)t * a.ldo + a.col + f;
-                            *(u32x2*)o = u32x2{pack2(v[0], v[1]), pack2(v[2], v[3])};
-                        }
                     }
+                    put(tl, fl / 4, v);
                 }
+        }
+    }
+
+    const long col0 = a.col + (GEGLU ? fw0 / 2 : fw0);
+    if constexpr (F32OUT) {
+        // 16 lanes per 256-byte row, 4 rows per pass.
+        const int q = lane & 15;
+#pragma unroll 4
+        for (int rr = lane >> 4; rr < 64; rr += 4) {
+            const int t = tw0 + rr;
+            if (t >= a.rows) break;
+            const f32x4 v = *(const f32x4*)&stage[rr * OW + ((q ^ oswz<CPR>(rr)) * 4)];
+            float* o = (float*)a.out + (long)t * a.ldo + col0 + q * 4;
+            if constexpr (EPI == JH_EPI_RESID_F32) {
+                f32x4 old = *(const f32x4*)o;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) old[e] += v[e];
+                *(f32x4*)o = old;
+            } else {
+                *(f32x4*)o = v;
             }
+        }
+    } else {
+        // OW/8 lanes per bf16 output row (16 bytes each), 64/(OW/8) rows per pass.
+        constexpr int LPR = OW / 8, RPP = 64 / LPR;
+        const int q = lane % LPR;
+#pragma unroll 4
+        for (int rr = lane / LPR; rr < 64; rr += RPP) {
+            const int t = tw0 + rr;
+            if (t >= a.rows) break;
+            const f32x4 v0 = *(const f32x4*)&stage[rr * OW + (((2 * q) ^ oswz<CPR>(rr)) * 4)];
+            const f32x4 v1 = *(const f32x4*)&stage[rr * OW + (((2 * q + 1) ^ oswz<CPR>(rr)) * 4)];
+            *(u32x4*)((bf16_t*)a.out + (long)t * a.ldo + col0 + q * 8) =
+                u32x4{pack2(v0[0], v0[1]), pack2(v0[2], v0[3]), pack2(v1[0], v1[1]), pack2(v1[2], v1[3])};
         }
     }
 }
 
-template <int EPI, int BF, int BT, int WF, int WT>
-__global__ __launch_bounds__(WF* WT * 64) void gemm_kernel(GemmArgs a) {
-    constexpr int NT = WF * WT * 64;
-    constexpr int FPW = BF / WF, TPW = BT / WT;  // features / tokens per wave
-    constexpr int FB = FPW / 32, TB = TPW / 32;  // 32x32 MFMA blocks per wave
-    constexpr int CW = BF * 8 / NT, CX = BT * 8 / NT;  // 16-byte chunks per thread per K step
-    static_assert(CW * NT == BF * 8 && CX * NT == BT * 8, "tile must split evenly over threads");
-    static_assert(FB >= 1 && TB >= 1, "wave tile too small");
-    static_assert((EPI != JH_EPI_ROPE_BF16 && EPI != JH_EPI_GEGLU_BF16) || FB % 2 == 0,
-                  "pair epilogues need 64-feature wave slabs");
+// Stages LDS through direct global->LDS DMA: each global_load_lds_dwordx4
+// writes 64 lanes x 16 B to one contiguous 1 KB LDS block (lane i at +16i,
+// verified on gfx950), so LDS rows cannot be padded; instead lane i loads the
+// global chunk that belongs in its slot under an XOR swizzle (physical chunk =
+// logical chunk ^ ((row >> 1) & 7) for 128-byte rows).  Measured on gfx950, a
+// 16-byte-per-lane LDS read runs at full rate only when each quarter-wave
+// (16 lanes) touches 256 distinct bytes of the 64 x 4-byte banks: with this
+// swizzle the 16 rows a quarter-wave reads fall into 16 distinct (row parity,
+// chunk) slots.  The plain row & 7 swizzle puts rows r and r+8 on the same
+// banks and halves LDS read bandwidth.  The DMA is issued
+// with inline asm so the compiler does not insert its conservative
+// vmcnt(0) before every LDS read; the wait for a stage is explicit.
+template <int EPI>
+__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
+    constexpr int BF = 128, BT = 128, FB = 2, TB = 2, NS = 2;
+    constexpr int CPR = BK / 8;           // 16-byte chunks per row (8)
+    constexpr int RPI = 64 / CPR;         // rows per 1 KB DMA instruction (8)
+    constexpr int IPW = BF / RPI / 4;     // DMA instructions per wave per operand per stage (4)
+    constexpr int STAGE = BF * BK;        // bf16 elements per operand per stage
+    // Operand stages during the K loop; the four waves' 16 KB epilogue staging
+    // rows afterwards.
+    __shared__ __align__(1024) bf16_t smem[2 * NS * STAGE];
+    bf16_t* const sW = smem;
+    bf16_t* const sX = smem + NS * STAGE;
 
-    __shared__ __align__(16) bf16_t sW[2][BF][LDS_STRIDE];
-    __shared__ __align__(16) bf16_t sX[2][BT][LDS_STRIDE];
-
-    const int tid = threadIdx.x;
-    const int nF = (a.n + BF - 1) / BF;
-    const int nTk = (a.rows + BT - 1) / BT;
-    const int ntiles = nF * nTk;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nF = (a.n + BF - 1) / BF, nTk = (a.rows + BT - 1) / BT, ntiles = nF * nTk;
     const int b = blockIdx.x;
     const int xcd = b & 7, local = b >> 3, q8 = ntiles >> 3, r8 = ntiles & 7;
     const int tile = xcd * q8 + (xcd < r8 ? xcd : r8) + local;
@@ -156,54 +185,34 @@ __global__ __launch_bounds__(WF* WT * 64) void gemm_kernel(GemmArgs a) {
     const int gh = min(GROUP, nTk - grp * GROUP);
     const int f0 = (gi / gh) * BF, t0 = (grp * GROUP + gi % gh) * BT;
 
-    // Per-thread source rows for the global->LDS copies (fixed across K steps).
-    // Rows past the end are clamped onto the last valid row: their products
-    // land in accumulator rows the epilogue never stores, and the loads stay
-    // unconditional, which keeps the compiler's vmcnt tracking exact (a
-    // branch around a load makes it wait for every load in flight).
-    const bf16_t* wsrc[CW];
-    const bf16_t* xsrc[CX];
+    // Per-lane DMA sources: rows past the end are clamped onto the last valid
+    // row (their products land in accumulator rows the epilogue never stores).
+    const bf16_t* wsrc[IPW];
+    const bf16_t* xsrc[IPW];
 #pragma unroll
-    for (int i = 0; i < CW; ++i) {
-        int c = tid + NT * i, row = c >> 3, kc = c & 7;
-        int f = min(f0 + row, a.n - 1);
-        wsrc[i] = a.w + (long)f * a.k + kc * 8;
+    for (int j = 0; j < IPW; ++j) {
+        const int lrow = (wave * IPW + j) * RPI + lane / CPR;
+        const int c = (lane % CPR) ^ swz(lrow);
+        wsrc[j] = a.w + (long)min(f0 + lrow, a.n - 1) * a.k + c * 8;
+        const int t = min(t0 + lrow, a.rows - 1);
+        const long src = a.gather ? (long)a.gather[t] : (long)t;
+        xsrc[j] = a.x + src * a.ldx + c * 8;
     }
-#pragma unroll
-    for (int i = 0; i < CX; ++i) {
-        int c = tid + NT * i, row = c >> 3, kc = c & 7;
-        int t = min(t0 + row, a.rows - 1);
-        long src = a.gather ? (long)a.gather[t] : (long)t;
-        xsrc[i] = a.x + src * a.ldx + kc * 8;
-    }
-
-    struct Stage {
-        u32x4 w[CW], x[CX];
-    };
-    auto gload = [&](Stage& s, int kt) {
+    // LDS byte offsets (low 32 bits of the generic LDS address) of this wave's blocks.
+    const uint32_t wl0 = (uint32_t)(uintptr_t)&sW[wave * IPW * 512];
+    const uint32_t xl0 = (uint32_t)(uintptr_t)&sX[wave * IPW * 512];
+    auto issue = [&](int kt, int st) {
         const int kb = kt * BK;
 #pragma unroll
-        for (int i = 0; i < CW; ++i) s.w[i] = *(const u32x4*)(wsrc[i] + kb);
-#pragma unroll
-        for (int i = 0; i < CX; ++i) s.x[i] = *(const u32x4*)(xsrc[i] + kb);
-    };
-    auto sstore = [&](const Stage& s, int buf) {
-#pragma unroll
-        for (int i = 0; i < CW; ++i) {
-            int c = tid + NT * i;
-            *(u32x4*)&sW[buf][c >> 3][(c & 7) * 8] = s.w[i];
-        }
-#pragma unroll
-        for (int i = 0; i < CX; ++i) {
-            int c = tid + NT * i;
-            *(u32x4*)&sX[buf][c >> 3][(c & 7) * 8] = s.x[i];
+        for (int j = 0; j < IPW; ++j) {
+            const uint32_t lw = __builtin_amdgcn_readfirstlane(wl0 + (st * STAGE + j * 512) * 2);
+            const uint32_t lx = __builtin_amdgcn_readfirstlane(xl0 + (st * STAGE + j * 512) * 2);
+            asm volatile("global_load_lds_dwordx4 %1, off" ::"{m0}"(lw), "v"(wsrc[j] + kb) : "memory");
+            asm volatile("global_load_lds_dwordx4 %1, off" ::"{m0}"(lx), "v"(xsrc[j] + kb) : "memory");
         }
     };
 
-    const int lane = tid & 63, wave = tid >> 6;
-    const int wf = wave % WF, wt = wave / WF;
-    const int lr = lane & 31, lk = (lane >> 5) * 8;
-
+    const int wf = wave & 1, wt = wave >> 1, lr = lane & 31, lg = lane >> 5;
     f32x16 acc[FB][TB];
 #pragma unroll
     for (int i = 0; i < FB; ++i)
@@ -212,50 +221,41 @@ __global__ __launch_bounds__(WF* WT * 64) void gemm_kernel(GemmArgs a) {
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-    auto compute = [&](int buf) {
+    // Step kt: wait for this wave's DMA of stage kt%2, barrier (all waves' data
+    // landed, and everyone finished reading the other stage), then start the
+    // DMA of step kt+1 into the other stage and run the MFMAs of step kt.
+    const int KT = a.k / BK;
+    issue(0, 0);
+    for (int kt = 0; kt < KT; ++kt) {
+        const int st = kt & 1;
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (kt + 1 < KT) issue(kt + 1, st ^ 1);
+        const bf16_t* W = sW + st * STAGE;
+        const bf16_t* X = sX + st * STAGE;
 #pragma unroll
         for (int ks = 0; ks < BK / 16; ++ks) {
+            const int c = ks * 2 + lg;
             bf16x8 af[FB], bx[TB];
 #pragma unroll
-            for (int i = 0; i < FB; ++i) af[i] = *(const bf16x8*)&sW[buf][wf * FPW + i * 32 + lr][ks * 16 + lk];
+            for (int i = 0; i < FB; ++i) {
+                const int r = wf * 64 + i * 32 + lr;
+                af[i] = *(const bf16x8*)&W[r * BK + ((c ^ swz(r)) * 8)];
+            }
 #pragma unroll
-            for (int j = 0; j < TB; ++j) bx[j] = *(const bf16x8*)&sX[buf][wt * TPW + j * 32 + lr][ks * 16 + lk];
+            for (int j = 0; j < TB; ++j) {
+                const int r = wt * 64 + j * 32 + lr;
+                bx[j] = *(const bf16x8*)&X[r * BK + ((c ^ swz(r)) * 8)];
+            }
 #pragma unroll
             for (int i = 0; i < FB; ++i)
 #pragma unroll
                 for (int j = 0; j < TB; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bx[j], acc[i][j], 0, 0, 0);
         }
-    };
-
-    // K steps kt = 0..KT-1.  Tile kt is loaded into register stage kt%2 two
-    // steps ahead and stored to LDS buffer kt%2 at the end of step kt-1.  The
-    // prefetch index is clamped instead of skipped near the end (re-reading the
-    // last tile from L2) so the steady-state loop carries no branches.
-    const int KT = a.k / BK;
-    Stage r0, r1;
-    gload(r0, 0);
-    gload(r1, min(1, KT - 1));
-    sstore(r0, 0);
-    __syncthreads();
-    gload(r0, min(2, KT - 1));
-    // One step: compute from LDS buf; stage `nxt` holds tile kt+1 -> LDS buf^1;
-    // then refill `nxt` with tile kt+3.
-    auto step = [&](int kt, Stage& nxt) {
-        const int buf = kt & 1;
-        compute(buf);
-        sstore(nxt, buf ^ 1);
-        gload(nxt, min(kt + 3, KT - 1));
-        __syncthreads();
-    };
-    int kt = 0;
-    for (; kt + 1 < KT; kt += 2) {
-        step(kt, r1);
-        step(kt + 1, r0);
     }
-    if (kt < KT) compute(kt & 1);
-
-    epilogue<EPI, FB, TB>(a, acc, f0 + wf * FPW, t0 + wt * TPW, lane);
+    __syncthreads();  // every wave is done reading the operand stages
+    if (f0 + wf * 64 < a.n) epilogue<EPI>(a, acc, f0 + wf * 64, t0 + wt * 64, lane, (float*)smem + wave * 4096);
 }
 
 // Tile shape: 128 features x 128 tokens, four waves of 64x64, two resident
@@ -268,7 +268,7 @@ template <int EPI>
 void launch_cfg(const GemmArgs& a, hipStream_t s) {
     constexpr int BF = 128, BT = 128;
     const int blocks = ((a.n + BF - 1) / BF) * ((a.rows + BT - 1) / BT);
-    JH_LAUNCH((gemm_kernel<EPI, BF, BT, 2, 2>), dim3(blocks), dim3(256), 0, s, a);
+    JH_LAUNCH((gemm_kernel<EPI>), dim3(blocks), dim3(256), 0, s, a);
     HIP_CHECK(hipGetLastError());
 }
 
@@ -283,8 +283,9 @@ void launch_gemm(int epi, const GemmArgs& a, hipStream_t s) {
         throw jh_error(1, "gemm: x/w must be 16-byte aligned with ldx % 8 == 0 and ldx >= K");
     const bool f32out = epi == JH_EPI_RESID_F32 || epi == JH_EPI_BIAS_F32;
     const long width = epi == JH_EPI_GEGLU_BF16 ? a.n / 2 : a.n;
-    if (a.col < 0 || a.ldo < a.col + width || a.ldo % 4 || a.col % 4 || ((uintptr_t)a.out & (f32out ? 15 : 7)))
-        throw jh_error(1, "gemm: output columns out of range or misaligned");
+    const int per16 = f32out ? 4 : 8;  // elements per 16-byte store
+    if (a.col < 0 || a.ldo < a.col + width || a.ldo % per16 || a.col % per16 || ((uintptr_t)a.out & 15))
+        throw jh_error(1, "gemm: output columns out of range, or rows/columns not 16-byte aligned");
     const bool needs_bias = epi == JH_EPI_BIAS_BF16 || epi == JH_EPI_BIAS_RELU_BF16 || epi == JH_EPI_BIAS_F32;
     if (needs_bias && !a.bias) throw jh_error(1, "gemm: epilogue needs a bias");
     if (epi == JH_EPI_ROPE_BF16 && a.rope_cols > 0 && (!a.pos || !a.cos_t || !a.sin_t || a.rope_cols % 64))

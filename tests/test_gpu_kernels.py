@@ -38,11 +38,11 @@ SHAPES = [(1, 64, 64), (37, 128, 768), (130, 384, 1152), (257, 2304, 768), (64, 
 @pytest.mark.parametrize("rows,n,k", SHAPES)
 def test_gemm_store_bf16(rows, n, k):
     x, w, ref = _gemm_inputs(rng(1), rows, n, k)
-    out = torch.zeros(rows, n + 8, dtype=BF16, device="cuda")
-    hip.op_gemm(abi.EPI_STORE_BF16, dev(x, BF16), dev(w, BF16), out, col=4)
+    out = torch.zeros(rows, n + 16, dtype=BF16, device="cuda")
+    hip.op_gemm(abi.EPI_STORE_BF16, dev(x, BF16), dev(w, BF16), out, col=8)
     got = host(out)
-    assert np.all(got[:, :4] == 0) and np.all(got[:, 4 + n:] == 0)
-    d = np.abs(got[:, 4:4 + n] - ref)
+    assert np.all(got[:, :8] == 0) and np.all(got[:, 8 + n:] == 0)
+    d = np.abs(got[:, 8:8 + n] - ref)
     assert np.all(d <= 4e-3 * np.abs(ref) + 1e-6), d.max()
 
 
@@ -134,6 +134,11 @@ def test_gemm_rejects_bad_shapes():
     out = torch.zeros(4, 64, dtype=BF16, device="cuda")
     with pytest.raises(hip.HipError):
         hip.op_gemm(abi.EPI_STORE_BF16, x, w, out)
+    # output column not on a 16-byte boundary
+    x = torch.zeros(4, 64, dtype=BF16, device="cuda")
+    out = torch.zeros(4, 72, dtype=BF16, device="cuda")
+    with pytest.raises(hip.HipError):
+        hip.op_gemm(abi.EPI_STORE_BF16, x, w, out, col=4)
 
 
 @pytest.mark.parametrize("hidden", [128, 384, 768])
