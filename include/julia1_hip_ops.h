@@ -101,7 +101,7 @@ int jh_op_scorer(const float* z, size_t rows, size_t hidden, const float* w2, fl
  * Attention work item: `nq` query rows starting at absolute row `q_row` attend
  * to `kv_len` key/value rows starting at `kv_row`; the first query sits at
  * sequence position `q_pos` (keys are at positions 0..kv_len-1), which is what
- * the sliding window measures against.  nq <= 64.
+ * the sliding window measures against.  nq <= 128.
  */
 typedef struct jh_attn_tile {
     int32_t q_row, nq, kv_row, kv_len, q_pos;

@@ -101,7 +101,7 @@ struct HeadLayer {
     DevBuf norm1_w, norm1_b, in_w, in_b, out_w, out_b, norm2_w, norm2_b, lin1_w, lin1_b, lin2_w, lin2_b;
 };
 
-constexpr int QTILE = 64;  // queries per attention work item
+constexpr int QTILE = 128;  // queries per attention work item (four waves of 32)
 
 // Kernel classes of the launch sequence, for jh_profile_read.
 enum KClass {
@@ -256,7 +256,7 @@ struct jh_model {
         if (next != t) throw jh_error(JH_ERR_INVALID, "sequence lengths do not sum to the token count");
         for (size_t i = 0; i < t; ++i)
             if (ids[i] >= (uint32_t)vocab) throw jh_error(JH_ERR_INVALID, "token id out of vocabulary");
-        // Attention work items: 64-query tiles per sequence; marker tiles per sequence.
+        // Attention work items: 128-query tiles per sequence; marker tiles per sequence.
         std::vector<AttnTile> tiles, mtiles;
         for (size_t s = 0; s < nseq; ++s)
             for (uint32_t q0 = 0; q0 < lens[s]; q0 += QTILE)

@@ -228,16 +228,17 @@ def _tiles(lens, qt=64):
     return tiles
 
 
+@pytest.mark.parametrize("qt", [64, 128])
 @pytest.mark.parametrize("window", [-1, 64, 8, 0])
-def test_attention_varlen(window):
+def test_attention_varlen(window, qt):
     r = rng(9)
     heads = 3
     h = heads * 64
-    lens = [1, 5, 63, 64, 65, 200, 300]
+    lens = [1, 5, 63, 64, 65, 127, 128, 129, 200, 300]
     t = sum(lens)
     qkv = bf16_round(r.standard_normal((t, 3 * h), dtype=np.float32))
     q, k, v = qkv[:, :h], qkv[:, h:2 * h], qkv[:, 2 * h:]
-    tiles = _tiles(lens)
+    tiles = _tiles(lens, qt)
     seqs = []
     start = 0
     for ln in lens:
