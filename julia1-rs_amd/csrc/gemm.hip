@@ -8,10 +8,11 @@
 // what the epilogues want: 16-byte FP32 residual read-modify-writes, and the
 // RoPE pair (d, d+32) and the GEGLU pair (gate, up) in the same lane.
 //
-// Pipeline: workgroup tile 256 features x 128 tokens x BK=64, eight waves of
-// 64x64.  Operands go global -> LDS by DMA (no register staging), three
-// stages: the DMA of K step kt+2 runs under the MFMAs of step kt, one barrier
-// per step, one workgroup per CU.
+// Pipeline: workgroup tile 128 features x 128 tokens x BK=64, four waves of
+// 64x64.  Operands go global -> LDS by buffer DMA (no register staging),
+// double-buffered: the DMA of K step kt+1 runs under the MFMAs of step kt,
+// one barrier per step, two resident workgroups per CU (64 KB LDS each); the
+// epilogue stages the tile through the same LDS for row-contiguous stores.
 //
 // Tiles are dealt XCD-contiguously: MI355X hands workgroups round-robin to its
 // 8 XCDs, so tile t goes to the workgroup whose id mod 8 selects the XCD that
@@ -154,133 +155,125 @@ __device__ inline i32x4 make_rsrc(const void* base, uint64_t bytes) {
                  0x00020000};
 }
 
-// Operands reach LDS by DMA: buffer_load_dwordx4 ... lds (and, for row-gathered
-// X, global_load_lds_dwordx4 with per-lane 64-bit addresses) writes 64 lanes x
-// 16 B to one contiguous 1 KB LDS block at M0 (lane i at +16i, verified on
-// gfx950).  The buffer form takes per-lane 32-bit offsets from a per-tile base
-// plus a scalar K offset; measured on MI355X it sustains ~15% more MFMA
-// throughput alongside the LDS reads than the 64-bit global form.  LDS rows
-// cannot be padded, so lane i loads the global chunk that belongs in its slot
-// under an XOR swizzle (physical chunk = logical chunk ^ ((row >> 1) & 7) for
-// 128-byte rows).  Measured on gfx950, a 16-byte-per-lane LDS read runs at
-// full rate only when each quarter-wave (16 lanes) touches 256 distinct bytes
-// of the 64 x 4-byte banks: with this swizzle the 16 rows a quarter-wave reads
-// fall into 16 distinct (row parity, chunk) slots (the plain row & 7 swizzle
-// puts rows r and r+8 on the same banks and halves LDS read bandwidth).  The
-// DMA is issued with inline asm so the compiler does not insert its
-// conservative vmcnt(0) before every LDS read; the wait for a stage is explicit.
-//
-// Workgroup: 8 waves, tile 256 features x 128 tokens (4 x 2 waves of 64 x 64),
-// three 48 KB stages (144 KB of LDS, one workgroup per CU).  The DMA of step
-// kt+2 is in flight while step kt computes.  Against two resident 128 x 128
-// workgroups per CU this moves 384 instead of 512 DMA bytes per MFMA, which
-// is what limits the LDS/MFMA overlap on MI355X.
+// Operands reach LDS by DMA: buffer_load_dwordx4 ... lds (global_load_lds_dwordx4
+// with 64-bit per-lane addresses for row-gathered X) writes 64 lanes x 16 B to
+// one contiguous 1 KB LDS block at M0 (lane i at +16i, verified on gfx950).
+// The buffer form (per-lane 32-bit offsets from a per-tile base, scalar K
+// offset) measured ~8% faster than the 64-bit global form in this kernel.
+// LDS rows cannot be padded, so lane i loads the global chunk that belongs in
+// its slot under an XOR swizzle (physical chunk = logical chunk ^ ((row >> 1)
+// & 7) for 128-byte rows).  Measured on gfx950, a 16-byte-per-lane LDS read
+// runs at full rate only when each quarter-wave (16 lanes) touches 256
+// distinct bytes of the 64 x 4-byte banks: with this swizzle the 16 rows a
+// quarter-wave reads fall into 16 distinct (row parity, chunk) slots (the
+// plain row & 7 swizzle puts rows r and r+8 on the same banks and halves LDS
+// read bandwidth).  The DMA is issued with inline asm so the compiler does not
+// insert its conservative vmcnt(0) before every LDS read; the wait for a stage
+// is explicit.
 template <int EPI, bool GATHER>
-__global__ __launch_bounds__(512) void gemm_kernel(GemmArgs a) {
-    constexpr int BF = 256, BT = 128, NS = 3, NW = 8;
-    constexpr int R = BF + BT;        // operand rows per stage: W rows, then X rows
-    constexpr int IPW = R / 8 / NW;   // 1 KB DMA instructions per wave per stage (6)
-    constexpr int STAGE = R * BK;     // bf16 elements per stage
-    static_assert(R / 8 % NW == 0, "DMA split");
-    // Operand stages during the K loop; the eight waves' 16 KB epilogue
-    // staging rows afterwards.
-    __shared__ __align__(1024) bf16_t smem[NS * STAGE];
+__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
+    constexpr int BF = 128, BT = 128, FB = 2, TB = 2, NS = 2;
+    constexpr int CPR = BK / 8;           // 16-byte chunks per row (8)
+    constexpr int RPI = 64 / CPR;         // rows per 1 KB DMA instruction (8)
+    constexpr int IPW = BF / RPI / 4;     // DMA instructions per wave per operand per stage (4)
+    constexpr int STAGE = BF * BK;        // bf16 elements per operand per stage
+    // Operand stages during the K loop; the four waves' 16 KB epilogue staging
+    // rows afterwards.
+    __shared__ __align__(1024) bf16_t smem[2 * NS * STAGE];
+    bf16_t* const sW = smem;
+    bf16_t* const sX = smem + NS * STAGE;
 
-    // wave is uniform across the wave; readfirstlane lets the compiler keep
-    // what derives from it (the per-instruction buffer resource) in SGPRs.
-    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nF = (a.n + BF - 1) / BF, nTk = (a.rows + BT - 1) / BT, ntiles = nF * nTk;
     const int b = blockIdx.x;
     const int xcd = b & 7, local = b >> 3, q8 = ntiles >> 3, r8 = ntiles & 7;
     const int tile = xcd * q8 + (xcd < r8 ? xcd : r8) + local;
     // Grouped order inside an XCD's band: GROUP token blocks are swept for
-    // each feature block, so the tiles resident on one XCD share about GROUP
-    // token blocks and a few feature blocks of operands in its L2.
+    // each feature block, so the ~64 tiles resident on one XCD share about
+    // GROUP token blocks and 64/GROUP feature blocks of operands in its L2.
     constexpr int GROUP = 8;
     const int grp = tile / (GROUP * nF), gi = tile - grp * GROUP * nF;
     const int gh = min(GROUP, nTk - grp * GROUP);
     const int f0 = (gi / gh) * BF, t0 = (grp * GROUP + gi % gh) * BT;
 
-    // Instruction j of wave w fills stage rows (w*IPW + j)*8 .. +7; lane i
-    // takes row +i/8, slot i%8.  Rows past the end are clamped onto the last
-    // valid row (their products land in accumulator rows never stored).
-    const bf16_t* xw = a.w + (long)f0 * a.k;
-    const bf16_t* xx = a.x + (long)t0 * a.ldx;
-    const i32x4 rw = make_rsrc(xw, (uint64_t)(a.n - f0) * a.k * 2);
-    const i32x4 rx = make_rsrc(xx, (uint64_t)(a.rows - 1 - t0) * a.ldx * 2 + (uint64_t)a.k * 2);
-    uint32_t voff[IPW];
-    const bf16_t* gsrc[GATHER ? IPW : 1];
+    // Per-lane DMA sources: rows past the end are clamped onto the last valid
+    // row (their products land in accumulator rows the epilogue never stores).
+    // W (and X unless row-gathered) load through buffer resources based at the
+    // tile (32-bit per-lane offsets plus a scalar K offset); gathered X rows
+    // use 64-bit per-lane addresses.
+    const bf16_t* wt0 = a.w + (long)f0 * a.k;
+    const bf16_t* xt0 = a.x + (long)t0 * a.ldx;
+    const i32x4 rw = make_rsrc(wt0, (uint64_t)(a.n - f0) * a.k * 2);
+    const i32x4 rx = make_rsrc(xt0, (uint64_t)(a.rows - 1 - t0) * a.ldx * 2 + (uint64_t)a.k * 2);
+    uint32_t woff[IPW], xoff[IPW];
+    const bf16_t* xsrc[GATHER ? IPW : 1];
 #pragma unroll
     for (int j = 0; j < IPW; ++j) {
-        const int row = (wave * IPW + j) * 8 + (lane >> 3);
-        const int c = (lane & 7) ^ swz(row);
-        if (row < BF) {
-            const int f = min(f0 + row, a.n - 1) - f0;
-            voff[j] = (uint32_t)(f * a.k + c * 8) * 2;
-            if constexpr (GATHER) gsrc[j] = xw + voff[j] / 2;
-        } else {
-            const int t = min(t0 + row - BF, a.rows - 1);
-            if constexpr (GATHER) gsrc[j] = a.x + (long)a.gather[t] * a.ldx + c * 8;
-            voff[j] = (uint32_t)((t - t0) * (long)a.ldx + c * 8) * 2;
-        }
+        const int lrow = (wave * IPW + j) * RPI + lane / CPR;
+        const int c = (lane % CPR) ^ swz(lrow);
+        woff[j] = (uint32_t)((min(f0 + lrow, a.n - 1) - f0) * a.k + c * 8) * 2;
+        const int t = min(t0 + lrow, a.rows - 1);
+        if constexpr (GATHER) xsrc[j] = a.x + (long)a.gather[t] * a.ldx + c * 8;
+        else xoff[j] = (uint32_t)((t - t0) * (long)a.ldx + c * 8) * 2;
     }
-    // LDS byte offset (low 32 bits of the generic LDS address) of this wave's blocks.
-    const uint32_t l0 = (uint32_t)(uintptr_t)&smem[wave * IPW * 512];
+    // LDS byte offsets (low 32 bits of the generic LDS address) of this wave's blocks.
+    const uint32_t wl0 = (uint32_t)(uintptr_t)&sW[wave * IPW * 512];
+    const uint32_t xl0 = (uint32_t)(uintptr_t)&sX[wave * IPW * 512];
     auto issue = [&](int kt, int st) {
-        const uint32_t kb = (uint32_t)kt * BK * 2;
+        const uint32_t kb = (uint32_t)kt * BK * 2;  // bytes
 #pragma unroll
         for (int j = 0; j < IPW; ++j) {
-            const uint32_t l = __builtin_amdgcn_readfirstlane(l0 + (st * STAGE + j * 512) * 2);
-            const bool isw = (wave * IPW + j) * 8 < BF;  // wave-uniform
-            if (GATHER && !isw)
-                asm volatile("global_load_lds_dwordx4 %1, off" ::"{m0}"(l), "v"(gsrc[j] + kb / 2) : "memory");
+            const uint32_t lw = __builtin_amdgcn_readfirstlane(wl0 + (st * STAGE + j * 512) * 2);
+            const uint32_t lx = __builtin_amdgcn_readfirstlane(xl0 + (st * STAGE + j * 512) * 2);
+            asm volatile("buffer_load_dwordx4 %1, %2, %3 offen lds" ::"{m0}"(lw), "v"(woff[j]), "s"(rw), "s"(kb)
+                         : "memory");
+            if constexpr (GATHER)
+                asm volatile("global_load_lds_dwordx4 %1, off" ::"{m0}"(lx), "v"(xsrc[j] + kb / 2) : "memory");
             else
-                asm volatile("buffer_load_dwordx4 %1, %2, %3 offen lds" ::"{m0}"(l), "v"(voff[j]), "s"(isw ? rw : rx),
-                             "s"(kb)
+                asm volatile("buffer_load_dwordx4 %1, %2, %3 offen lds" ::"{m0}"(lx), "v"(xoff[j]), "s"(rx), "s"(kb)
                              : "memory");
         }
     };
 
-    const int wf = wave & 3, wt = wave >> 2, lr = lane & 31, lg = lane >> 5;
-    f32x16 acc[2][2];
+    const int wf = wave & 1, wt = wave >> 1, lr = lane & 31, lg = lane >> 5;
+    f32x16 acc[FB][TB];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < FB; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < TB; ++j)
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-    // Step kt: wait for this wave's DMA of stage kt (the next stage may stay in
-    // flight), barrier (all waves' data landed, everyone finished step kt-1),
-    // start the DMA of step kt+2 into the stage step kt-1 used, run step kt.
+    // Step kt: wait for this wave's DMA of stage kt%2, barrier (all waves' data
+    // landed, and everyone finished reading the other stage), then start the
+    // DMA of step kt+1 into the other stage and run the MFMAs of step kt.
     const int KT = a.k / BK;
     issue(0, 0);
-    if (KT > 1) issue(1, 1);
     for (int kt = 0; kt < KT; ++kt) {
-        if (kt + 1 < KT) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(IPW) : "memory");
-        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        const int st = kt & 1;
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
-        if (kt + 2 < KT) issue(kt + 2, (kt + 2) % NS);
-        const bf16_t* W = smem + (kt % NS) * STAGE;
-        const bf16_t* X = W + BF * BK;
+        if (kt + 1 < KT) issue(kt + 1, st ^ 1);
+        const bf16_t* W = sW + st * STAGE;
+        const bf16_t* X = sX + st * STAGE;
 #pragma unroll
         for (int ks = 0; ks < BK / 16; ++ks) {
             const int c = ks * 2 + lg;
-            bf16x8 af[2], bx[2];
+            bf16x8 af[FB], bx[TB];
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
+            for (int i = 0; i < FB; ++i) {
                 const int r = wf * 64 + i * 32 + lr;
                 af[i] = *(const bf16x8*)&W[r * BK + ((c ^ swz(r)) * 8)];
             }
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
+            for (int j = 0; j < TB; ++j) {
                 const int r = wt * 64 + j * 32 + lr;
                 bx[j] = *(const bf16x8*)&X[r * BK + ((c ^ swz(r)) * 8)];
             }
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < FB; ++i)
 #pragma unroll
-                for (int j = 0; j < 2; ++j)
+                for (int j = 0; j < TB; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bx[j], acc[i][j], 0, 0, 0);
         }
     }
@@ -288,11 +281,19 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmArgs a) {
     if (f0 + wf * 64 < a.n) epilogue<EPI>(a, acc, f0 + wf * 64, t0 + wt * 64, lane, (float*)smem + wave * 4096);
 }
 
+// Tile shape: 128 features x 128 tokens, four waves of 64x64, two resident
+// workgroups per CU (64 KB of LDS each).  Measured on MI355X against 256x128
+// (8 waves of 64x64, three 48 KB stages, one workgroup per CU; 384 instead of
+// 512 DMA bytes per MFMA) and 256x256 (8 waves of 128x64): in the encoder
+// forward they tie at config1 and lose ~10% at M = 16384, because the two
+// independent workgroups per CU hide each other's prologue, barrier waits and
+// epilogue, which a single workgroup per CU leaves exposed.
 template <int EPI>
 void launch_cfg(const GemmArgs& a, hipStream_t s) {
-    const int blocks = ((a.n + 255) / 256) * ((a.rows + 127) / 128);
-    if (a.gather) JH_LAUNCH((gemm_kernel<EPI, true>), dim3(blocks), dim3(512), 0, s, a);
-    else JH_LAUNCH((gemm_kernel<EPI, false>), dim3(blocks), dim3(512), 0, s, a);
+    constexpr int BF = 128, BT = 128;
+    const int blocks = ((a.n + BF - 1) / BF) * ((a.rows + BT - 1) / BT);
+    if (a.gather) JH_LAUNCH((gemm_kernel<EPI, true>), dim3(blocks), dim3(256), 0, s, a);
+    else JH_LAUNCH((gemm_kernel<EPI, false>), dim3(blocks), dim3(256), 0, s, a);
     HIP_CHECK(hipGetLastError());
 }
 
