@@ -178,6 +178,17 @@ typedef struct jh_kernel_stat {
 int jh_profile(jh_model* model, int enabled);
 int jh_profile_read(jh_model* model, jh_kernel_stat* out, size_t capacity, size_t* count);
 
+/*
+ * Device time of one launch of a GEMM or attention kernel class, without
+ * per-launch events: the first launch of that class recorded by the last
+ * profiled jh_execute is replayed `reps` times back to back between two
+ * events on the model's stream, and the mean is written to *us_per_launch.
+ * The replay reuses the staged workspace: a residual-epilogue GEMM adds into
+ * the residual stream again, so run it after the forward's scores were read
+ * (the next jh_execute recomputes everything).  No reference counterpart.
+ */
+int jh_profile_replay(jh_model* model, const char* kernel_class, size_t reps, double* us_per_launch);
+
 /* "hip:N (<device name>)" — replaces `CudaModel::name` (src/cuda/mod.rs:252,278-280). */
 const char* jh_name(jh_model* model);
 

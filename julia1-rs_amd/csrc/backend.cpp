@@ -6,6 +6,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <functional>
 #include <memory>
 #include <mutex>
 #include <string>
@@ -169,6 +170,9 @@ struct jh_model {
     std::vector<hipEvent_t> ev_pool;
     size_t ev_next = 0;
     std::vector<ProfRec> recs;
+    // profiling: the first GEMM / attention launch of each class, kept by
+    // value so jh_profile_replay can repeat it back to back
+    std::function<void()> replay[K_COUNT];
 
     ~jh_model() {
         if (graph) (void)hipGraphExecDestroy(graph);
@@ -242,6 +246,8 @@ struct jh_model {
     // Validates and uploads a packed batch (Batch, src/model.rs:114-124).
     void stage(const uint32_t* ids, size_t t, const uint32_t* starts, const uint32_t* lens, const uint8_t* qtypes,
                size_t nseq, const uint32_t* marker_rows, size_t m) {
+        // Recorded replays point into the staged batch's metadata and workspace.
+        for (auto& r : replay) r = nullptr;
         if ((t && !ids) || (nseq && (!starts || !lens || !qtypes)) || (m && !marker_rows))
             throw jh_error(JH_ERR_INVALID, "null batch array");
         if (t > (size_t)0x7fffffff || m > (size_t)0x7fffffff) throw jh_error(JH_ERR_INVALID, "batch too large");
@@ -312,6 +318,7 @@ struct jh_model {
         GemmArgs a{(const bf16_t*)xp, ldx, gather, (int)rows, w, n, k, out, ldo, col, bias,
                    (const int32_t*)d_tok, cos_t, sin_t, rope_cols};
         timed(cls, 2.0 * rows * n * k, gemm_bytes(epi, rows, n, k), [&] { launch_gemm(epi, a, stream); });
+        if (profiling && !replay[cls]) replay[cls] = [epi, a, st = stream] { launch_gemm(epi, a, st); };
     }
 
     void attention(int cls, const bf16_t* q, long ldq, const bf16_t* k, const bf16_t* v, long ldkv, bf16_t* out,
@@ -319,6 +326,7 @@ struct jh_model {
         AttnArgs a{q, ldq, k, v, ldkv, out, ldo, tiles, (int)n, nheads, window, 0.125f * 1.4426950408889634f};
         const double hd = 64.0 * nheads;
         timed(cls, 4.0 * hd * pairs, qrows * hd * 2 * 2 + (double)T * hd * 2 * 2, [&] { launch_attention(a, stream); });
+        if (profiling && !replay[cls]) replay[cls] = [a, st = stream] { launch_attention(a, st); };
     }
 
     void layer_norm(int cls, const float* xp, size_t rows, const float* w, const float* b, float e, bf16_t* out) {
@@ -623,6 +631,39 @@ int jh_profile(jh_model* model, int enabled) {
         model->profiling = enabled != 0;
         model->recs.clear();
         model->ev_next = 0;
+        for (auto& r : model->replay) r = nullptr;
+    });
+}
+
+int jh_profile_replay(jh_model* model, const char* kernel_class, size_t reps, double* us_per_launch) {
+    return jh_guarded([&] {
+        if (!model || !kernel_class || !us_per_launch || reps == 0) throw jh_error(JH_ERR_INVALID, "bad argument");
+        std::lock_guard<std::mutex> g(model->mu);
+        int cls = -1;
+        for (int c = 0; c < K_COUNT; ++c)
+            if (std::strcmp(kClassNames[c], kernel_class) == 0) cls = c;
+        if (cls < 0 || !model->replay[cls])
+            throw jh_error(JH_ERR_INVALID, "no recorded GEMM/attention launch of that class (profile a forward first)");
+        model->bind();
+        hipEvent_t e0, e1;
+        HIP_CHECK(hipEventCreate(&e0));
+        HIP_CHECK(hipEventCreate(&e1));
+        float ms = 0.0f;
+        try {
+            model->replay[cls]();  // warm
+            HIP_CHECK(hipEventRecord(e0, model->stream));
+            for (size_t i = 0; i < reps; ++i) model->replay[cls]();
+            HIP_CHECK(hipEventRecord(e1, model->stream));
+            HIP_CHECK(hipEventSynchronize(e1));
+            HIP_CHECK(hipEventElapsedTime(&ms, e0, e1));
+        } catch (...) {
+            (void)hipEventDestroy(e0);
+            (void)hipEventDestroy(e1);
+            throw;
+        }
+        (void)hipEventDestroy(e0);
+        (void)hipEventDestroy(e1);
+        *us_per_launch = 1e3 * (double)ms / (double)reps;
     });
 }
 

@@ -18,7 +18,7 @@ _lib = None
 EXPORTS = (
     "jh_create", "jh_forward", "jh_forward_padded", "jh_stage", "jh_execute", "jh_scores", "jh_stream",
     "jh_set_graph", "jh_name", "jh_destroy", "jh_last_error", "jh_rope_table", "jh_debug_tokens",
-    "jh_debug_encode", "jh_profile", "jh_profile_read",
+    "jh_debug_encode", "jh_profile", "jh_profile_read", "jh_profile_replay",
     "jh_op_gemm", "jh_op_interleave_geglu", "jh_op_embed_ln", "jh_op_layer_norm", "jh_op_final_norm",
     "jh_op_gather_f32", "jh_op_scorer", "jh_op_attention",
 )
@@ -63,6 +63,7 @@ def lib():
         L.jh_debug_encode.argtypes = [vp, u32, vp, sz]
         L.jh_profile.argtypes = [vp, C.c_int]
         L.jh_profile_read.argtypes = [vp, vp, sz, C.POINTER(sz)]
+        L.jh_profile_replay.argtypes = [vp, C.c_char_p, sz, C.POINTER(C.c_double)]
         L.jh_op_gemm.argtypes = [C.c_int, vp, sz, vp, sz, vp, sz, sz, vp, sz, sz, vp, vp, vp, vp, sz, vp]
         L.jh_op_interleave_geglu.argtypes = [vp, sz, sz, vp]
         L.jh_op_interleave_geglu.restype = None
@@ -166,6 +167,13 @@ class HipModel:
         check(lib().jh_profile_read(self.h, arr, 32, C.byref(n)))
         return [dict(name=arr[i].name.decode(), launches=arr[i].launches, ms=arr[i].ms, flops=arr[i].flops,
                      bytes=arr[i].bytes) for i in range(n.value)]
+
+    def profile_replay(self, kernel_class: str, reps: int = 50) -> float:
+        """Mean device µs of one launch of a GEMM/attention class, replayed back to back
+        (see jh_profile_replay); valid right after a profiled forward."""
+        us = C.c_double()
+        check(lib().jh_profile_replay(self.h, kernel_class.encode(), reps, C.byref(us)))
+        return us.value
 
     def close(self):
         if getattr(self, "h", None) and _lib is not None:

@@ -194,3 +194,25 @@ def test_base_long_sequence_8192(base):
     s = parity(b, gpu.forward(b), orc.forward(b))
     print("config3[0]", s)
     check_gates(s)
+
+
+def test_profile_replay(tiny):
+    """jh_profile_replay times a recorded GEMM/attention launch; staging a batch drops the record."""
+    ws, gpu, orc = tiny
+    b = synth.make_batch([40, 17, 130], [3, 2, 5], ws.cfg.vocab, 3)
+    gpu.stage(b)
+    gpu.profile(True)
+    gpu.execute()
+    names = {s["name"] for s in gpu.profile_read()}
+    assert "gemm_qkv_rope" in names
+    assert gpu.profile_replay("gemm_qkv_rope", 5) > 0
+    assert gpu.profile_replay("attn_global", 5) > 0
+    with pytest.raises(hip.HipError):
+        gpu.profile_replay("layer_norm", 5)   # not a replayable class
+    gpu.stage(b)
+    with pytest.raises(hip.HipError):
+        gpu.profile_replay("gemm_qkv_rope", 5)
+    gpu.profile(False)
+    # the model still computes the same scores afterwards
+    s = parity(b, gpu.forward(b), orc.forward(b))
+    check_gates(s)
