@@ -71,18 +71,22 @@ __global__ __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(3))) void 
     constexpr int KCH = KT * 8 / NTHR;   // 16-byte K chunks per thread
     constexpr int VUN = KT * 4 / NTHR;   // (key pair, 8 dims) V units per thread
     u32x4 rk[KCH], rv[VUN][2];
+    // Rows past the sequence end are clamped onto its last key, so every load
+    // is unconditional (a branch around a load makes the compiler wait for all
+    // loads in flight); those keys are masked to -inf before the softmax, and
+    // their V rows are finite, so they contribute exactly 0.
     auto gload = [&](int k0) {
 #pragma unroll
         for (int i = 0; i < KCH; ++i) {
-            int c = tid + NTHR * i, key = c >> 3, dc = c & 7;
-            rk[i] = k0 + key < kend ? *(const u32x4*)(kbase + (long)(k0 + key) * a.ldkv + dc * 8) : u32x4{0, 0, 0, 0};
+            int c = tid + NTHR * i, key = min(k0 + (c >> 3), kend - 1), dc = c & 7;
+            rk[i] = *(const u32x4*)(kbase + (long)key * a.ldkv + dc * 8);
         }
 #pragma unroll
         for (int i = 0; i < VUN; ++i) {
             int u = tid + NTHR * i, pr = u & 31, dc = u >> 5;
             int key = k0 + 2 * pr;
-            rv[i][0] = key < kend ? *(const u32x4*)(vbase + (long)key * a.ldkv + dc * 8) : u32x4{0, 0, 0, 0};
-            rv[i][1] = key + 1 < kend ? *(const u32x4*)(vbase + (long)(key + 1) * a.ldkv + dc * 8) : u32x4{0, 0, 0, 0};
+            rv[i][0] = *(const u32x4*)(vbase + (long)min(key, kend - 1) * a.ldkv + dc * 8);
+            rv[i][1] = *(const u32x4*)(vbase + (long)min(key + 1, kend - 1) * a.ldkv + dc * 8);
         }
     };
     auto sstore = [&](int buf) {
@@ -113,7 +117,6 @@ __global__ __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(3))) void 
     const float c = a.scale_log2;
     // Queries of this wave sit at positions [qlo, qlo + 31].
     const int qlo = tile.q_pos + wave * 32;
-    const unsigned w2 = 2u * (unsigned)a.window;
 
     const int ntk = kend > kbeg ? (kend - kbeg + KT - 1) / KT : 0;
     if (ntk > 0) {
@@ -154,15 +157,23 @@ __global__ __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(3))) void 
         const bool tail = k0 + KT > kend;
         const bool edge = a.window >= 0 && (k0 < qlo + 31 - a.window || k0 + KT - 1 > qlo + a.window);
         if (tail || edge) {
-            const int kl = k0 + 4 * g;     // key of element 0 in block 0 for this lane
-            const int dq = qpos - kl;      // query - key for element 0
+            // Element offset off (key kl + off) is valid iff lo <= off <= hi:
+            // off < kend - kl, and |qpos - kl - off| <= window when windowed.
+            const int kl = k0 + 4 * g;  // key of element 0 in block 0 for this lane
+            int lo = 0, hi = kend - kl - 1;
+            if (a.window >= 0) {
+                lo = max(lo, qpos - kl - a.window);
+                hi = min(hi, qpos - kl + a.window);
+            }
+            // Empty range: move lo far right so off - lo wraps to a huge value.
+            const unsigned span = hi >= lo ? (unsigned)(hi - lo) : 0u;
+            lo = hi >= lo ? lo : 0x40000000;
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
                     const int off = kb * 32 + (e >> 2) * 8 + (e & 3);
-                    bool ok = kl + off < kend;
-                    if (a.window >= 0) ok = ok && (unsigned)(dq - off + a.window) <= w2;
+                    const bool ok = (unsigned)(off - lo) <= span;
                     s[kb][e] = ok ? s[kb][e] : -INFINITY;
                 }
         }
@@ -173,7 +184,7 @@ __global__ __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(3))) void 
             for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[kb][e]);
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
         const float mn = fmaxf(m, mx);
-        if (__any(mn > m)) {  // rescale only when some running max moved
+        {  // rescale unconditionally: straight-line code keeps O in place
             const float alpha = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m - mn) * c);
             l *= alpha;
 #pragma unroll
