@@ -53,6 +53,19 @@ int jh_op_gemm(int epilogue, const void* x, size_t ldx, const int32_t* gather, s
                const float* bias, const int32_t* pos, const float* cos_t, const float* sin_t,
                size_t rope_cols, void* stream);
 
+/*
+ * jh_op_gemm with split-K: K is cut into `splits` chunks (0 = chosen from the
+ * tile count, as the backend does for small batches) whose FP32 partial sums
+ * go to `workspace` (splits · rows · N floats must fit `workspace_bytes`;
+ * fewer splits are used otherwise), then one more kernel sums them in chunk
+ * order and applies the epilogue.  Deterministic.  Same requirements as
+ * jh_op_gemm.  No reference counterpart (cuBLAS chooses its own split-K).
+ */
+int jh_op_gemm_splitk(int epilogue, const void* x, size_t ldx, const int32_t* gather, size_t rows,
+                      const void* w, size_t n, size_t k, void* out, size_t ldo, size_t col,
+                      const float* bias, const int32_t* pos, const float* cos_t, const float* sin_t,
+                      size_t rope_cols, void* workspace, size_t workspace_bytes, int splits, void* stream);
+
 /* Reorder a host FP32 Wi [2*inter, k] into the gate/up interleave JH_EPI_GEGLU_BF16 expects. */
 void jh_op_interleave_geglu(const float* wi, size_t inter, size_t k, float* out);
 

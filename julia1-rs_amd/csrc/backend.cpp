@@ -150,6 +150,10 @@ struct jh_model {
     uint64_t ws_gen = 0;
     DevBuf x, xn, qkv, ctx, hbuf, y, yn, qm, cm, hm, z, scores, meta;
     PinnedBuf meta_host, scores_host;
+    // split-K partial sums of GEMMs whose output has too few tiles (small
+    // batches, marker rows): fixed size, allocated with the model
+    static constexpr size_t kSplitkBytes = 24u << 20;
+    DevBuf splitk;
     // staged batch
     bool staged = false;
     size_t T = 0, S = 0, M = 0, ntiles = 0, nmtiles = 0;
@@ -160,6 +164,8 @@ struct jh_model {
     int32_t* d_markers = nullptr;
     // graph of the launch sequence for the staged shape
     bool use_graph = true;
+    // split-K GEMMs for outputs with too few tiles (see jh_set_splitk)
+    bool use_splitk = true;
     hipGraphExec_t graph = nullptr;
     size_t graph_key[6] = {0, 0, 0, 0, 0, 0};
     std::string name;
@@ -317,6 +323,10 @@ struct jh_model {
               const float* sin_t = nullptr, int rope_cols = 0) {
         GemmArgs a{(const bf16_t*)xp, ldx, gather, (int)rows, w, n, k, out, ldo, col, bias,
                    (const int32_t*)d_tok, cos_t, sin_t, rope_cols};
+        if (use_splitk) {
+            a.partial = splitk.as<float>();
+            a.partial_bytes = kSplitkBytes;
+        }
         timed(cls, 2.0 * rows * n * k, gemm_bytes(epi, rows, n, k), [&] { launch_gemm(epi, a, stream); });
         if (profiling && !replay[cls]) replay[cls] = [epi, a, st = stream] { launch_gemm(epi, a, st); };
     }
@@ -518,6 +528,7 @@ void build_model(jh_model* m, const jh_config* c, const jh_weights* w, int ordin
     std::string arch = prop.gcnArchName;
     arch = arch.substr(0, arch.find(':'));
     m->name = "hip:" + std::to_string(ordinal) + " (" + dev_name + ", " + arch + ")";
+    m->splitk.alloc(jh_model::kSplitkBytes);
     HIP_CHECK(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking));
     const size_t H = c->hidden, I = c->intermediate, F = c->head_ff;
     m->h = (int)H; m->heads = (int)c->heads; m->inter = (int)I; m->nlayers = (int)c->layers;
@@ -619,6 +630,17 @@ int jh_set_graph(jh_model* model, int enabled) {
         if (!model) throw jh_error(JH_ERR_INVALID, "null model");
         std::lock_guard<std::mutex> g(model->mu);
         model->use_graph = enabled != 0;
+    });
+}
+
+int jh_set_splitk(jh_model* model, int enabled) {
+    return jh_guarded([&] {
+        if (!model) throw jh_error(JH_ERR_INVALID, "null model");
+        std::lock_guard<std::mutex> g(model->mu);
+        if (model->use_splitk != (enabled != 0)) {
+            model->use_splitk = enabled != 0;
+            ++model->ws_gen;  // the captured graph holds the other launch sequence
+        }
     });
 }
 

@@ -20,12 +20,19 @@
 // the operands resident on one XCD fit its 4 MB L2.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include "../../include/julia1_hip_ops.h"
 #include "kernels.hpp"
 
 namespace {
 
 constexpr int BK = 64;
+
+// Internal epilogue of the split-K partial pass: raw FP32 accumulators to the
+// workspace (no bias), reduced and finished by splitk_reduce.
+constexpr int EPI_PARTIAL = 100;
+constexpr int SPLITK_MAX = 16;  // most K chunks of one split-K GEMM
 
 // LDS chunk swizzle of operand row r (see gemm_kernel).
 __device__ constexpr int swz(int r) { return (r >> 1) & 7; }
@@ -47,7 +54,8 @@ __device__ constexpr int oswz(int r) {
 template <int EPI>
 __device__ inline void epilogue(const GemmArgs& a, f32x16 (&acc)[2][2], int fw0, int tw0, int lane, float* stage) {
     constexpr bool GEGLU = EPI == JH_EPI_GEGLU_BF16;
-    constexpr bool F32OUT = EPI == JH_EPI_RESID_F32 || EPI == JH_EPI_BIAS_F32;
+    constexpr bool F32OUT = EPI == JH_EPI_RESID_F32 || EPI == JH_EPI_BIAS_F32 || EPI == EPI_PARTIAL;
+    constexpr bool BIASED = EPI == JH_EPI_BIAS_BF16 || EPI == JH_EPI_BIAS_RELU_BF16 || EPI == JH_EPI_BIAS_F32;
     constexpr int OW = GEGLU ? 32 : 64;  // output columns of the wave tile
     constexpr int CPR = OW / 4;          // 16-byte FP32 chunks per staging row
     const int g4 = (lane >> 5) * 4, lr = lane & 31;
@@ -100,7 +108,7 @@ __device__ inline void epilogue(const GemmArgs& a, f32x16 (&acc)[2][2], int fw0,
                     f32x4 v;
 #pragma unroll
                     for (int e = 0; e < 4; ++e) v[e] = acc[i][j][qd * 4 + e];
-                    if (EPI != JH_EPI_STORE_BF16 && (EPI != JH_EPI_RESID_F32 || a.bias)) {
+                    if (BIASED || (EPI == JH_EPI_RESID_F32 && a.bias)) {
                         const f32x4 bb = *(const f32x4*)(a.bias + fw0 + fl);
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
@@ -185,7 +193,10 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nF = (a.n + BF - 1) / BF, nTk = (a.rows + BT - 1) / BT, ntiles = nF * nTk;
-    const int b = blockIdx.x;
+    // Split-K partial pass: workgroup blockIdx.x covers tile blockIdx.x % ntiles
+    // and K steps [split·kt_chunk, (split+1)·kt_chunk).
+    const int split = EPI == EPI_PARTIAL ? (int)blockIdx.x / ntiles : 0;
+    const int b = EPI == EPI_PARTIAL ? (int)blockIdx.x - split * ntiles : (int)blockIdx.x;
     const int xcd = b & 7, local = b >> 3, q8 = ntiles >> 3, r8 = ntiles & 7;
     const int tile = xcd * q8 + (xcd < r8 ? xcd : r8) + local;
     // Grouped order inside an XCD's band: GROUP token blocks are swept for
@@ -247,10 +258,11 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
     // Step kt: wait for this wave's DMA of stage kt%2, barrier (all waves' data
     // landed, and everyone finished reading the other stage), then start the
     // DMA of step kt+1 into the other stage and run the MFMAs of step kt.
-    const int KT = a.k / BK;
-    issue(0, 0);
-    for (int kt = 0; kt < KT; ++kt) {
-        const int st = kt & 1;
+    const int kt0 = EPI == EPI_PARTIAL ? split * a.kt_chunk : 0;
+    const int KT = EPI == EPI_PARTIAL ? min(a.k / BK, kt0 + a.kt_chunk) : a.k / BK;
+    issue(kt0, 0);
+    for (int kt = kt0; kt < KT; ++kt) {
+        const int st = (kt - kt0) & 1;
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         if (kt + 1 < KT) issue(kt + 1, st ^ 1);
@@ -278,7 +290,105 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
         }
     }
     __syncthreads();  // every wave is done reading the operand stages
-    if (f0 + wf * 64 < a.n) epilogue<EPI>(a, acc, f0 + wf * 64, t0 + wt * 64, lane, (float*)smem + wave * 4096);
+    if (f0 + wf * 64 >= a.n) return;
+    if constexpr (EPI == EPI_PARTIAL) {
+        GemmArgs e = a;
+        e.out = a.partial + (size_t)split * a.rows * a.n;
+        e.ldo = a.n;
+        e.col = 0;
+        epilogue<EPI>(e, acc, f0 + wf * 64, t0 + wt * 64, lane, (float*)smem + wave * 4096);
+    } else {
+        epilogue<EPI>(a, acc, f0 + wf * 64, t0 + wt * 64, lane, (float*)smem + wave * 4096);
+    }
+}
+
+// Split-K reduction + epilogue: thread (row t, 64-wide slab, q) sums the S
+// partials of columns slab + 4q .. +3 and slab + 32 + 4q .. +3 in split order
+// and applies the same elementwise epilogue, with the same expression order,
+// as the GEMM's own epilogue.
+template <int EPI>
+__global__ __launch_bounds__(256) void splitk_reduce(GemmArgs a, int S) {
+    const long id = (long)blockIdx.x * 256 + threadIdx.x;
+    const int slabs = a.n / 64;
+    const long t = id / (slabs * 8);
+    if (t >= a.rows) return;
+    const int rem = (int)(id - t * slabs * 8), slab = (rem >> 3) * 64, q = rem & 7;
+    const size_t plane = (size_t)a.rows * a.n;
+    const float* p = a.partial + (size_t)t * a.n + slab + 4 * q;
+    // All partial loads first (unconditional: planes past S re-read plane
+    // S-1 and are not added), then the sums in split order.
+    f32x4 pl[SPLITK_MAX], ph[SPLITK_MAX];
+#pragma unroll
+    for (int s = 0; s < SPLITK_MAX; ++s) {
+        const float* ps = p + (size_t)min(s, S - 1) * plane;
+        pl[s] = *(const f32x4*)ps;
+        ph[s] = *(const f32x4*)(ps + 32);
+    }
+    f32x4 lo = pl[0], hi = ph[0];
+#pragma unroll
+    for (int s = 1; s < SPLITK_MAX; ++s)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            lo[e] = s < S ? lo[e] + pl[s][e] : lo[e];
+            hi[e] = s < S ? hi[e] + ph[s][e] : hi[e];
+        }
+    auto store_bf16 = [&](long col, f32x4 v) {
+        *(u32x2*)((bf16_t*)a.out + t * a.ldo + col) = u32x2{pack2(v[0], v[1]), pack2(v[2], v[3])};
+    };
+    const long c0 = a.col + slab + 4 * q;
+    if constexpr (EPI == JH_EPI_ROPE_BF16) {
+        if (slab < a.rope_cols) {
+            const long ps = (long)(a.pos[t] & 0xffff) * 32 + 4 * q;
+            const f32x4 c = *(const f32x4*)(a.cos_t + ps), sn = *(const f32x4*)(a.sin_t + ps);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float x0 = lo[e], x1 = hi[e];
+                lo[e] = x0 * c[e] - x1 * sn[e];
+                hi[e] = x1 * c[e] + x0 * sn[e];
+            }
+        }
+        store_bf16(c0, lo);
+        store_bf16(c0 + 32, hi);
+    } else if constexpr (EPI == JH_EPI_GEGLU_BF16) {
+        f32x4 g;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) g[e] = gelu_erf(lo[e]) * hi[e];
+        store_bf16(a.col + slab / 2 + 4 * q, g);
+    } else {
+        const bool biased = EPI == JH_EPI_BIAS_BF16 || EPI == JH_EPI_BIAS_RELU_BF16 || EPI == JH_EPI_BIAS_F32 ||
+                            (EPI == JH_EPI_RESID_F32 && a.bias);
+        if (biased) {
+            const f32x4 bl = *(const f32x4*)(a.bias + slab + 4 * q), bh = *(const f32x4*)(a.bias + slab + 32 + 4 * q);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                lo[e] += bl[e];
+                hi[e] += bh[e];
+                if constexpr (EPI == JH_EPI_BIAS_RELU_BF16) {
+                    lo[e] = fmaxf(lo[e], 0.0f);
+                    hi[e] = fmaxf(hi[e], 0.0f);
+                }
+            }
+        }
+        if constexpr (EPI == JH_EPI_RESID_F32 || EPI == JH_EPI_BIAS_F32) {
+            float* o = (float*)a.out + t * a.ldo + c0;
+            if constexpr (EPI == JH_EPI_RESID_F32) {
+                f32x4 ol = *(const f32x4*)o, oh = *(const f32x4*)(o + 32);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    ol[e] += lo[e];
+                    oh[e] += hi[e];
+                }
+                *(f32x4*)o = ol;
+                *(f32x4*)(o + 32) = oh;
+            } else {
+                *(f32x4*)o = lo;
+                *(f32x4*)(o + 32) = hi;
+            }
+        } else {
+            store_bf16(c0, lo);
+            store_bf16(c0 + 32, hi);
+        }
+    }
 }
 
 // Tile shape: 128 features x 128 tokens, four waves of 64x64, two resident
@@ -288,10 +398,38 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
 // forward they tie at config1 and lose ~10% at M = 16384, because the two
 // independent workgroups per CU hide each other's prologue, barrier waits and
 // epilogue, which a single workgroup per CU leaves exposed.
+// Split count for an output of `tiles` 128x128 tiles: enough workgroups to
+// cover the GPU about once (256 CUs x 2 resident) when the tile count alone
+// leaves most CUs idle, at least two 64-deep K steps per split, and the
+// partials must fit the workspace.
+int splitk_count(const GemmArgs& a, long tiles) {
+    const int kt = a.k / BK;
+    if (!a.partial) return 1;
+    int s = a.splits > 0 ? a.splits : (tiles >= 128 ? 1 : (int)((384 + tiles - 1) / tiles));
+    s = std::min({s, kt / 2, SPLITK_MAX});
+    while (s > 1 && (size_t)s * a.rows * a.n * sizeof(float) > a.partial_bytes) --s;
+    if (s <= 1) return 1;
+    const int chunk = (kt + s - 1) / s;
+    return (kt + chunk - 1) / chunk;
+}
+
 template <int EPI>
 void launch_cfg(const GemmArgs& a, hipStream_t s) {
     constexpr int BF = 128, BT = 128;
     const int blocks = ((a.n + BF - 1) / BF) * ((a.rows + BT - 1) / BT);
+    const int S = splitk_count(a, blocks);
+    if (S > 1) {
+        GemmArgs p = a;
+        const int kt = a.k / BK;
+        p.kt_chunk = (kt + S - 1) / S;
+        if (a.gather) JH_LAUNCH((gemm_kernel<EPI_PARTIAL, true>), dim3(blocks * S), dim3(256), 0, s, p);
+        else JH_LAUNCH((gemm_kernel<EPI_PARTIAL, false>), dim3(blocks * S), dim3(256), 0, s, p);
+        HIP_CHECK(hipGetLastError());
+        const long threads = (long)a.rows * (a.n / 64) * 8;
+        JH_LAUNCH((splitk_reduce<EPI>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, p, S);
+        HIP_CHECK(hipGetLastError());
+        return;
+    }
     if (a.gather) JH_LAUNCH((gemm_kernel<EPI, true>), dim3(blocks), dim3(256), 0, s, a);
     else JH_LAUNCH((gemm_kernel<EPI, false>), dim3(blocks), dim3(256), 0, s, a);
     HIP_CHECK(hipGetLastError());

@@ -40,6 +40,16 @@ struct GemmArgs {
     const float* cos_t;     // ROPE: [positions, 32]
     const float* sin_t;
     int rope_cols;          // ROPE: columns [0, rope_cols) are rotated
+    // Split-K (optional): a device workspace for FP32 partial sums.  When the
+    // output has too few tiles to fill the GPU, launch_gemm splits K into
+    // chunks written to `partial` and reduces them, in a fixed order, in a
+    // second kernel that applies the epilogue.  `splits` > 0 forces that many
+    // chunks (tests); 0 chooses automatically; null `partial` disables it.
+    float* partial = nullptr;
+    size_t partial_bytes = 0;
+    int splits = 0;
+    // set by launch_gemm for the split-K partial pass
+    int kt_chunk = 0;
 };
 
 void launch_gemm(int epilogue, const GemmArgs& a, hipStream_t stream);

@@ -28,6 +28,22 @@ int jh_op_gemm(int epilogue, const void* x, size_t ldx, const int32_t* gather, s
     });
 }
 
+int jh_op_gemm_splitk(int epilogue, const void* x, size_t ldx, const int32_t* gather, size_t rows, const void* w,
+                      size_t n, size_t k, void* out, size_t ldo, size_t col, const float* bias, const int32_t* pos,
+                      const float* cos_t, const float* sin_t, size_t rope_cols, void* workspace,
+                      size_t workspace_bytes, int splits, void* stream) {
+    return jh_guarded([&] {
+        if (!workspace || ((uintptr_t)workspace & 15)) throw jh_error(1, "gemm: split-K needs a 16-byte aligned workspace");
+        GemmArgs a{(const bf16_t*)x, (long)ldx, gather, as_int(rows, "rows"), (const bf16_t*)w, as_int(n, "n"),
+                   as_int(k, "k"), out, (long)ldo, as_int(col, "col"), bias, pos, cos_t, sin_t,
+                   as_int(rope_cols, "rope_cols")};
+        a.partial = (float*)workspace;
+        a.partial_bytes = workspace_bytes;
+        a.splits = splits;
+        launch_gemm(epilogue, a, (hipStream_t)stream);
+    });
+}
+
 void jh_op_interleave_geglu(const float* wi, size_t inter, size_t k, float* out) {
     for (size_t j = 0; j < inter / 32; ++j)
         for (size_t r = 0; r < 32; ++r) {

@@ -17,9 +17,9 @@ _lib = None
 
 EXPORTS = (
     "jh_create", "jh_forward", "jh_forward_padded", "jh_stage", "jh_execute", "jh_scores", "jh_stream",
-    "jh_set_graph", "jh_name", "jh_destroy", "jh_last_error", "jh_rope_table", "jh_debug_tokens",
+    "jh_set_graph", "jh_set_splitk", "jh_name", "jh_destroy", "jh_last_error", "jh_rope_table", "jh_debug_tokens",
     "jh_debug_encode", "jh_profile", "jh_profile_read", "jh_profile_replay",
-    "jh_op_gemm", "jh_op_interleave_geglu", "jh_op_embed_ln", "jh_op_layer_norm", "jh_op_final_norm",
+    "jh_op_gemm", "jh_op_gemm_splitk", "jh_op_interleave_geglu", "jh_op_embed_ln", "jh_op_layer_norm", "jh_op_final_norm",
     "jh_op_gather_f32", "jh_op_scorer", "jh_op_attention",
 )
 
@@ -51,6 +51,7 @@ def lib():
         L.jh_stream.argtypes = [vp]
         L.jh_stream.restype = vp
         L.jh_set_graph.argtypes = [vp, C.c_int]
+        L.jh_set_splitk.argtypes = [vp, C.c_int]
         L.jh_name.argtypes = [vp]
         L.jh_name.restype = C.c_char_p
         L.jh_destroy.argtypes = [vp]
@@ -65,6 +66,8 @@ def lib():
         L.jh_profile_read.argtypes = [vp, vp, sz, C.POINTER(sz)]
         L.jh_profile_replay.argtypes = [vp, C.c_char_p, sz, C.POINTER(C.c_double)]
         L.jh_op_gemm.argtypes = [C.c_int, vp, sz, vp, sz, vp, sz, sz, vp, sz, sz, vp, vp, vp, vp, sz, vp]
+        L.jh_op_gemm_splitk.argtypes = [C.c_int, vp, sz, vp, sz, vp, sz, sz, vp, sz, sz, vp, vp, vp, vp, sz, vp, sz,
+                                        C.c_int, vp]
         L.jh_op_interleave_geglu.argtypes = [vp, sz, sz, vp]
         L.jh_op_interleave_geglu.restype = None
         L.jh_op_embed_ln.argtypes = [vp, sz, vp, vp, C.c_float, sz, vp, vp, vp]
@@ -142,6 +145,9 @@ class HipModel:
     def set_graph(self, on: bool):
         check(lib().jh_set_graph(self.h, 1 if on else 0))
 
+    def set_splitk(self, on: bool):
+        check(lib().jh_set_splitk(self.h, 1 if on else 0))
+
     @property
     def stream(self) -> int:
         return lib().jh_stream(self.h) or 0
@@ -197,6 +203,16 @@ def op_gemm(epi, x, w, out, rows=None, gather=None, col=0, bias=None, pos=None, 
     n, k = w.shape
     check(lib().jh_op_gemm(epi, _dp(x), x.stride(0), _dp(gather), rows, _dp(w), n, k, _dp(out), out.stride(0), col,
                            _dp(bias), _dp(pos), _dp(cos), _dp(sin), rope_cols, stream))
+
+
+def op_gemm_splitk(epi, x, w, out, workspace, splits=0, rows=None, gather=None, col=0, bias=None, pos=None, cos=None,
+                   sin=None, rope_cols=0, stream=None):
+    """jh_op_gemm_splitk: like op_gemm with a torch workspace tensor for the FP32 partials."""
+    rows = x.shape[0] if rows is None else rows
+    n, k = w.shape
+    check(lib().jh_op_gemm_splitk(epi, _dp(x), x.stride(0), _dp(gather), rows, _dp(w), n, k, _dp(out), out.stride(0),
+                                  col, _dp(bias), _dp(pos), _dp(cos), _dp(sin), rope_cols, _dp(workspace),
+                                  workspace.numel() * workspace.element_size(), splits, stream))
 
 
 def interleave_geglu(wi: np.ndarray) -> np.ndarray:

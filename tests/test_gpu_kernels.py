@@ -128,6 +128,75 @@ def test_gemm_rope(theta):
     assert np.all(d <= 4e-3 * scale + 1e-6), d.max()
 
 
+@pytest.mark.parametrize("splits", [0, 2, 5])
+@pytest.mark.parametrize("epi", [abi.EPI_STORE_BF16, abi.EPI_ROPE_BF16, abi.EPI_GEGLU_BF16, abi.EPI_RESID_F32,
+                                 abi.EPI_BIAS_BF16, abi.EPI_BIAS_RELU_BF16, abi.EPI_BIAS_F32])
+def test_gemm_splitk_matches_f64(epi, splits):
+    """Split-K (FP32 partials reduced in chunk order, then the epilogue) against the f64 product,
+    with the same per-epilogue tolerances as the single-pass GEMM; plus determinism."""
+    r = rng(12)
+    rows, n, k = 70, 384, 1152
+    x, w, ref = _gemm_inputs(r, rows, n, k)
+    bias = (r.standard_normal(n, dtype=np.float32) * 0.1).astype(np.float32)
+    pos = r.integers(0, 8192, rows).astype(np.int32)
+    cos, sin = oracle.rope_table(10000.0, 8192)
+    ws = torch.zeros(8 << 20, dtype=torch.uint8, device="cuda")
+    kw = {}
+    if epi == abi.EPI_ROPE_BF16:
+        kw = dict(pos=dev(pos), cos=dev(cos), sin=dev(sin), rope_cols=256)
+        expect = ref.copy()
+        scale = np.abs(ref).copy()
+        for hd in range(0, 256, 64):
+            a, b = ref[:, hd:hd + 32], ref[:, hd + 32:hd + 64]
+            c, s_ = cos[pos].astype(np.float64), sin[pos].astype(np.float64)
+            expect[:, hd:hd + 32] = a * c - b * s_
+            expect[:, hd + 32:hd + 64] = b * c + a * s_
+            scale[:, hd:hd + 64] = np.tile(np.abs(a) + np.abs(b), 2)
+    elif epi == abi.EPI_GEGLU_BF16:
+        wi = w
+        prod = x.astype(np.float64) @ wi.astype(np.float64).T
+        u, v = prod[:, :n // 2], prod[:, n // 2:]
+        erf = np.vectorize(math.erf)
+        expect = 0.5 * u * (1 + erf(u / math.sqrt(2))) * v
+        scale = np.abs(expect) + 1e-3 * np.abs(u * v)
+        w = hip.interleave_geglu(wi)
+    elif epi == abi.EPI_RESID_F32:
+        base = r.standard_normal((rows, n), dtype=np.float32)
+        kw = dict(bias=dev(bias))
+        expect = base + ref + bias
+    else:
+        kw = dict(bias=dev(bias)) if epi != abi.EPI_STORE_BF16 else {}
+        expect = ref + (bias if kw else 0)
+        if epi == abi.EPI_BIAS_RELU_BF16:
+            expect = np.maximum(expect, 0)
+    width = n // 2 if epi == abi.EPI_GEGLU_BF16 else n
+    f32 = epi in (abi.EPI_RESID_F32, abi.EPI_BIAS_F32)
+    outs = []
+    for _ in range(2):
+        out = dev(base) if epi == abi.EPI_RESID_F32 else torch.zeros(rows, width, dtype=torch.float32 if f32 else BF16,
+                                                                      device="cuda")
+        hip.op_gemm_splitk(epi, dev(x, BF16), dev(w, BF16), out, ws, splits=splits, **kw)
+        outs.append(host(out))
+    assert np.array_equal(outs[0], outs[1])  # fixed reduction order
+    d = np.abs(outs[0] - expect)
+    if f32:
+        assert d.max() < 1e-4, d.max()
+    else:
+        sc = scale if epi in (abi.EPI_ROPE_BF16, abi.EPI_GEGLU_BF16) else np.abs(expect)
+        assert np.all(d <= 4e-3 * sc + 2e-6), d.max()
+
+
+def test_gemm_splitk_gathered_rows():
+    r = rng(13)
+    x, w, ref = _gemm_inputs(r, 300, 256, 512)
+    idx = np.array([5, 0, 299, 17, 17, 100, 3], dtype=np.int32)
+    out = torch.zeros(idx.size, 256, dtype=torch.float32, device="cuda")
+    ws = torch.zeros(1 << 20, dtype=torch.uint8, device="cuda")
+    hip.op_gemm_splitk(abi.EPI_BIAS_F32, dev(x, BF16), dev(w, BF16), out, ws, splits=4, rows=idx.size,
+                       gather=dev(idx), bias=dev(np.zeros(256, dtype=np.float32)))
+    assert np.abs(host(out) - ref[idx]).max() < 1e-5
+
+
 def test_gemm_rejects_bad_shapes():
     x = torch.zeros(4, 100, dtype=BF16, device="cuda")
     w = torch.zeros(64, 100, dtype=BF16, device="cuda")
