@@ -238,6 +238,26 @@ def main():
                                                   / (ms * 1e-3), 4)))
         extra["gemm_sweep"] = sweep
         log("sweep:", sweep)
+        # Small request (configs[0], one 128-token row: launch/latency bound) and the router-scale
+        # varlen batch (configs[4], ~133k tokens): graph-replayed forwards and PCIe-inclusive calls.
+        for wl, reps in (("config0", 50), ("config4", 5)):
+            bw = synth.workload(wl)
+            model.stage(bw)
+            model.execute()
+            torch.cuda.synchronize()
+            tw = time.perf_counter()
+            for _ in range(reps):
+                model.execute()
+            torch.cuda.synchronize()
+            fw = (time.perf_counter() - tw) / reps * 1e3
+            tw = time.perf_counter()
+            for _ in range(reps):
+                model.forward(bw)
+            pw = (time.perf_counter() - tw) / reps * 1e3
+            extra[wl] = dict(tokens=bw.tokens, rows=int(bw.lens.size), markers=int(bw.marker_rows.size),
+                             forward_ms=round(fw, 3), forward_with_pcie_ms=round(pw, 3),
+                             tokens_per_s=round(bw.tokens / fw * 1e3))
+            log(f"{wl}: {bw.tokens} tokens, forward {fw:.3f} ms ({pw:.3f} ms with PCIe)")
 
     cpu = None
     parity = None
@@ -261,6 +281,16 @@ def main():
         parity = dict(max_dlogit=float(np.abs(gpu_scores - ref).max()),
                       argmax_agree=sum(int(np.argmax(a) == np.argmax(b)) for a, b in zip(gs, rs)), rows=len(gs))
         log(f"cpu oracle: {med:.2f} s/forward on {threads} threads; parity {parity}")
+        if not args.no_extra and threads != 4:
+            # The reference CPU path's default thread count (JULIA_CPU_THREADS=4, src/engine.rs:160-162).
+            orc4 = oracle.OracleModel(ws, threads=4)
+            t4 = []
+            for _ in range(3):
+                tc = time.perf_counter()
+                orc4.forward(batch)
+                t4.append(time.perf_counter() - tc)
+            cpu["value_4_threads"] = round(tokens / statistics.median(t4), 1)
+            log(f"cpu oracle: {statistics.median(t4):.2f} s/forward on 4 threads")
 
     out = {
         "metric": METRIC, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,

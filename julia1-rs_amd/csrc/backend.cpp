@@ -331,6 +331,34 @@ struct jh_model {
         if (profiling && !replay[cls]) replay[cls] = [epi, a, st = stream] { launch_gemm(epi, a, st); };
     }
 
+    // RESID_F32 GEMM into xo [rows, H] followed by lo = bf16(LN(xo)).  On the
+    // split-K path (small batches) the partial reduction, residual add and
+    // LayerNorm are one kernel; otherwise the GEMM epilogue adds the residual
+    // and a separate LayerNorm follows.
+    void gemm_resid_ln(int cls, int ln_cls, const void* xp, long ldx, size_t rows, const bf16_t* w, int k, float* xo,
+                       const float* bias, const float* ln_w, const float* ln_b, float ln_eps, bf16_t* lo) {
+        const int H = h;
+        GemmArgs a{(const bf16_t*)xp, ldx, nullptr, (int)rows, w, H, k, xo, H, 0, bias,
+                   (const int32_t*)d_tok, nullptr, nullptr, 0};
+        int S = 1;
+        if (use_splitk) {
+            a.partial = splitk.as<float>();
+            a.partial_bytes = kSplitkBytes;
+            S = gemm_splitk_count(JH_EPI_RESID_F32, a);
+        }
+        if (S <= 1) {
+            gemm(cls, JH_EPI_RESID_F32, xp, ldx, nullptr, rows, w, H, k, xo, H, 0, bias);
+            layer_norm(ln_cls, xo, rows, ln_w, ln_b, ln_eps, lo);
+            return;
+        }
+        timed(cls, 2.0 * rows * H * k, gemm_bytes(JH_EPI_RESID_F32, rows, H, k),
+              [&] { launch_gemm_partial(JH_EPI_RESID_F32, a, S, stream); });
+        if (profiling && !replay[cls]) replay[cls] = [a, S, st = stream] { launch_gemm_partial(JH_EPI_RESID_F32, a, S, st); };
+        timed(ln_cls, 0, (double)rows * H * (4.0 * S + 14), [&] {
+            launch_resid_reduce_ln(splitk.as<float>(), S, (int)rows, H, bias, xo, ln_w, ln_b, ln_eps, lo, stream);
+        });
+    }
+
     void attention(int cls, const bf16_t* q, long ldq, const bf16_t* k, const bf16_t* v, long ldkv, bf16_t* out,
                    long ldo, const AttnTile* tiles, size_t n, int nheads, int window, double pairs, double qrows) {
         AttnArgs a{q, ldq, k, v, ldkv, out, ldo, tiles, (int)n, nheads, window, 0.125f * 1.4426950408889634f};
@@ -351,9 +379,12 @@ struct jh_model {
             launch_embed_ln(d_ids, (int)t, emb.as<float>(), emb_norm.as<float>(), eps, H, x.as<float>(),
                             xn.as<bf16_t>(), stream);
         });
+        bool xn_ready = false;  // xn already holds this layer's attn_norm(x) (fused into the previous Wo2)
         for (int l = 0; l < upto; ++l) {
             EncLayer& L = layers[l];
-            if (L.attn_norm.p) layer_norm(K_LN, x.as<float>(), t, L.attn_norm.as<float>(), nullptr, eps, xn.as<bf16_t>());
+            if (L.attn_norm.p && !xn_ready)
+                layer_norm(K_LN, x.as<float>(), t, L.attn_norm.as<float>(), nullptr, eps, xn.as<bf16_t>());
+            xn_ready = false;
             gemm(K_QKV, JH_EPI_ROPE_BF16, xn.p, H, nullptr, t, L.wqkv.as<bf16_t>(), 3 * H, H, qkv.p, 3 * H, 0, nullptr,
                  ropes[L.rope].first.as<float>(), ropes[L.rope].second.as<float>(), 2 * H);
             const bf16_t* q = qkv.as<bf16_t>();
@@ -363,11 +394,18 @@ struct jh_model {
             else
                 attention(K_ATTN_LOCAL, q, 3 * H, q + H, q + 2 * H, 3 * H, ctx.as<bf16_t>(), H, d_tiles, ntiles, heads,
                           half_window, pairs_local, (double)t);
-            gemm(K_WO, JH_EPI_RESID_F32, ctx.p, H, nullptr, t, L.wo.as<bf16_t>(), H, H, x.p, H, 0, nullptr);
-            layer_norm(K_LN, x.as<float>(), t, L.mlp_norm.as<float>(), nullptr, eps, xn.as<bf16_t>());
+            gemm_resid_ln(K_WO, K_LN, ctx.p, H, t, L.wo.as<bf16_t>(), H, x.as<float>(), nullptr,
+                          L.mlp_norm.as<float>(), nullptr, eps, xn.as<bf16_t>());
             gemm(K_WI, JH_EPI_GEGLU_BF16, xn.p, H, nullptr, t, L.wi.as<bf16_t>(), 2 * inter, H, hbuf.p, inter, 0,
                  nullptr);
-            gemm(K_WO2, JH_EPI_RESID_F32, hbuf.p, inter, nullptr, t, L.wo2.as<bf16_t>(), H, inter, x.p, H, 0, nullptr);
+            if (l + 1 < upto && layers[l + 1].attn_norm.p) {
+                gemm_resid_ln(K_WO2, K_LN, hbuf.p, inter, t, L.wo2.as<bf16_t>(), inter, x.as<float>(), nullptr,
+                              layers[l + 1].attn_norm.as<float>(), nullptr, eps, xn.as<bf16_t>());
+                xn_ready = true;
+            } else {
+                gemm(K_WO2, JH_EPI_RESID_F32, hbuf.p, inter, nullptr, t, L.wo2.as<bf16_t>(), H, inter, x.p, H, 0,
+                     nullptr);
+            }
         }
     }
 
@@ -389,17 +427,13 @@ struct jh_model {
             const bf16_t* q = qkv.as<bf16_t>();
             attention(K_HEAD_ATTN, q, 3 * H, q + H, q + 2 * H, 3 * H, ctx.as<bf16_t>(), H, d_tiles, ntiles, head_heads,
                       -1, pairs_global, (double)t);
-            gemm(K_HEAD_GEMM, JH_EPI_RESID_F32, ctx.p, H, nullptr, t, L.out_w.as<bf16_t>(), H, H, x.p, H, 0,
-                 L.out_b.as<float>());
-            layer_norm(K_HEAD_ROWS, x.as<float>(), t, L.norm2_w.as<float>(), L.norm2_b.as<float>(), 1e-5f,
-                       xn.as<bf16_t>());
+            gemm_resid_ln(K_HEAD_GEMM, K_HEAD_ROWS, ctx.p, H, t, L.out_w.as<bf16_t>(), H, x.as<float>(),
+                          L.out_b.as<float>(), L.norm2_w.as<float>(), L.norm2_b.as<float>(), 1e-5f, xn.as<bf16_t>());
             gemm(K_HEAD_GEMM, JH_EPI_BIAS_RELU_BF16, xn.p, H, nullptr, t, L.lin1_w.as<bf16_t>(), ff, H, hbuf.p, ff, 0,
                  L.lin1_b.as<float>());
-            gemm(K_HEAD_GEMM, JH_EPI_RESID_F32, hbuf.p, ff, nullptr, t, L.lin2_w.as<bf16_t>(), H, ff, x.p, H, 0,
-                 L.lin2_b.as<float>());
             HeadLayer& N = head[j + 1];
-            layer_norm(K_HEAD_ROWS, x.as<float>(), t, N.norm1_w.as<float>(), N.norm1_b.as<float>(), 1e-5f,
-                       xn.as<bf16_t>());
+            gemm_resid_ln(K_HEAD_GEMM, K_HEAD_ROWS, hbuf.p, ff, t, L.lin2_w.as<bf16_t>(), ff, x.as<float>(),
+                          L.lin2_b.as<float>(), N.norm1_w.as<float>(), N.norm1_b.as<float>(), 1e-5f, xn.as<bf16_t>());
         }
         HeadLayer& L = head[nh - 1];
         // Keys/values for every token: in_proj rows [H, 3H) into qkv columns [H, 3H).
@@ -414,15 +448,13 @@ struct jh_model {
         timed(K_HEAD_ROWS, 0, (double)m * H * 8, [&] {
             launch_gather_f32(x.as<float>(), d_markers, (int)m, H, y.as<float>(), stream);
         });
-        gemm(K_HEAD_GEMM, JH_EPI_RESID_F32, cm.p, H, nullptr, m, L.out_w.as<bf16_t>(), H, H, y.p, H, 0,
-             L.out_b.as<float>());
-        layer_norm(K_HEAD_ROWS, y.as<float>(), m, L.norm2_w.as<float>(), L.norm2_b.as<float>(), 1e-5f, yn.as<bf16_t>());
+        gemm_resid_ln(K_HEAD_GEMM, K_HEAD_ROWS, cm.p, H, m, L.out_w.as<bf16_t>(), H, y.as<float>(),
+                      L.out_b.as<float>(), L.norm2_w.as<float>(), L.norm2_b.as<float>(), 1e-5f, yn.as<bf16_t>());
         gemm(K_HEAD_GEMM, JH_EPI_BIAS_RELU_BF16, yn.p, H, nullptr, m, L.lin1_w.as<bf16_t>(), ff, H, hm.p, ff, 0,
              L.lin1_b.as<float>());
-        gemm(K_HEAD_GEMM, JH_EPI_RESID_F32, hm.p, ff, nullptr, m, L.lin2_w.as<bf16_t>(), H, ff, y.p, H, 0,
-             L.lin2_b.as<float>());
-        // Scorer: LayerNorm -> Linear -> GELU -> Linear(.., 1).
-        layer_norm(K_SCORER, y.as<float>(), m, s_norm_w.as<float>(), s_norm_b.as<float>(), 1e-5f, yn.as<bf16_t>());
+        // Scorer: LayerNorm -> Linear -> GELU -> Linear(.., 1); its LayerNorm follows lin2's residual.
+        gemm_resid_ln(K_HEAD_GEMM, K_SCORER, hm.p, ff, m, L.lin2_w.as<bf16_t>(), ff, y.as<float>(),
+                      L.lin2_b.as<float>(), s_norm_w.as<float>(), s_norm_b.as<float>(), 1e-5f, yn.as<bf16_t>());
         gemm(K_SCORER, JH_EPI_BIAS_F32, yn.p, H, nullptr, m, s_w1.as<bf16_t>(), H, H, z.p, H, 0, s_b1.as<float>());
         timed(K_SCORER, 4.0 * m * H, (double)m * H * 4 + m * 4.0, [&] {
             launch_scorer(z.as<float>(), (int)m, H, s_w2.as<float>(), s_b2, scores.as<float>(), stream);

@@ -437,10 +437,14 @@ void launch_cfg(const GemmArgs& a, hipStream_t s) {
 
 }  // namespace
 
-void launch_gemm(int epi, const GemmArgs& a, hipStream_t s) {
+namespace {
+
+// Shape, alignment and argument checks shared by every GEMM entry; false when
+// there is nothing to do (rows == 0).
+bool validate_gemm(int epi, const GemmArgs& a) {
     if (a.rows < 0 || a.n <= 0 || a.k <= 0 || a.k % BK || a.n % 64 || a.k > 8192)
         throw jh_error(1, "gemm: need K % 64 == 0, N % 64 == 0, K <= 8192");
-    if (a.rows == 0) return;
+    if (a.rows == 0) return false;
     if (!a.x || !a.w || !a.out) throw jh_error(1, "gemm: null operand");
     if (a.ldx % 8 || a.ldx < a.k || ((uintptr_t)a.x & 15) || ((uintptr_t)a.w & 15))
         throw jh_error(1, "gemm: x/w must be 16-byte aligned with ldx % 8 == 0 and ldx >= K");
@@ -454,6 +458,34 @@ void launch_gemm(int epi, const GemmArgs& a, hipStream_t s) {
     if (epi == JH_EPI_ROPE_BF16 && a.rope_cols > 0 && (!a.pos || !a.cos_t || !a.sin_t || a.rope_cols % 64))
         throw jh_error(1, "gemm: RoPE epilogue needs pos, cos, sin and rope_cols % 64 == 0");
     if (epi == JH_EPI_GEGLU_BF16 && a.n % 64) throw jh_error(1, "gemm: GEGLU needs N % 64 == 0");
+    if (epi < JH_EPI_STORE_BF16 || epi > JH_EPI_BIAS_F32) throw jh_error(1, "gemm: unknown epilogue");
+    return true;
+}
+
+}  // namespace
+
+int gemm_splitk_count(int epi, const GemmArgs& a) {
+    if (!validate_gemm(epi, a)) return 1;
+    return splitk_count(a, (long)((a.n + 127) / 128) * ((a.rows + 127) / 128));
+}
+
+void launch_gemm_partial(int epi, const GemmArgs& a, int splits, hipStream_t s) {
+    if (!validate_gemm(epi, a)) return;
+    if (splits < 2 || !a.partial || (size_t)splits * a.rows * a.n * sizeof(float) > a.partial_bytes ||
+        splits > SPLITK_MAX || splits > a.k / BK)
+        throw jh_error(1, "gemm: split-K partial pass needs 2..16 splits fitting the workspace");
+    GemmArgs p = a;
+    const int kt = a.k / BK;
+    p.kt_chunk = (kt + splits - 1) / splits;
+    if ((kt + p.kt_chunk - 1) / p.kt_chunk != splits) throw jh_error(1, "gemm: split count leaves an empty K chunk");
+    const int blocks = ((a.n + 127) / 128) * ((a.rows + 127) / 128);
+    if (a.gather) JH_LAUNCH((gemm_kernel<EPI_PARTIAL, true>), dim3(blocks * splits), dim3(256), 0, s, p);
+    else JH_LAUNCH((gemm_kernel<EPI_PARTIAL, false>), dim3(blocks * splits), dim3(256), 0, s, p);
+    HIP_CHECK(hipGetLastError());
+}
+
+void launch_gemm(int epi, const GemmArgs& a, hipStream_t s) {
+    if (!validate_gemm(epi, a)) return;
     switch (epi) {
         case JH_EPI_STORE_BF16: launch_cfg<JH_EPI_STORE_BF16>(a, s); break;
         case JH_EPI_ROPE_BF16: launch_cfg<JH_EPI_ROPE_BF16>(a, s); break;

@@ -53,6 +53,11 @@ struct GemmArgs {
 };
 
 void launch_gemm(int epilogue, const GemmArgs& a, hipStream_t stream);
+// Split count launch_gemm would use for `a` (1 = no split-K), and the split-K
+// partial pass alone (FP32 partials [splits][rows][n] into a.partial), for
+// callers that fuse the reduction with what follows (launch_resid_reduce_ln).
+int gemm_splitk_count(int epilogue, const GemmArgs& a);
+void launch_gemm_partial(int epilogue, const GemmArgs& a, int splits, hipStream_t stream);
 
 struct AttnTile {
     int32_t q_row, nq, kv_row, kv_len, q_pos;
@@ -79,6 +84,8 @@ void launch_embed_ln(const uint32_t* ids, int rows, const float* table, const fl
                      float* x, bf16_t* xn, hipStream_t stream);
 void launch_layer_norm(const float* x, int rows, const float* w, const float* b, float eps, int hidden, bf16_t* out,
                        hipStream_t stream);
+void launch_resid_reduce_ln(const float* partial, int splits, int rows, int hidden, const float* bias, float* x,
+                            const float* w, const float* b, float eps, bf16_t* out, hipStream_t stream);
 void launch_final_norm(float* x, int rows, const float* fw, const float* type_emb, const uint32_t* tok_meta,
                        const float* hw, const float* hb, float eps, int hidden, bf16_t* out, hipStream_t stream);
 void launch_gather_f32(const float* src, const int32_t* idx, int rows, int hidden, float* dst, hipStream_t stream);

@@ -116,6 +116,47 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const float* __restrict
     r.store_bf16(out + (long)row * H, lane);
 }
 
+// Split-K residual GEMM finish fused with the LayerNorm that follows it:
+// x[row] += Σ_s partial[s][row] (+ bias), summed in split order exactly as
+// the GEMM's own split-K reduction does, then out = bf16(LN(x[row])).
+template <int EPL>
+__global__ __launch_bounds__(256) void resid_reduce_ln_kernel(const float* __restrict__ partial, int S, long plane,
+                                                              const float* __restrict__ bias, float* __restrict__ x,
+                                                              int rows, const float* __restrict__ w,
+                                                              const float* __restrict__ b, float eps,
+                                                              bf16_t* __restrict__ out) {
+    constexpr int H = EPL * 64;
+    const int row = blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const float* p = partial + (long)row * H;
+    RowVec<EPL> acc;
+    acc.load(p, lane);
+    // Four planes per round, loaded before they are added (planes past S
+    // re-read plane S-1 and are skipped).
+    for (int s0 = 1; s0 < S; s0 += 4) {
+        RowVec<EPL> t[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) t[u].load(p + (long)min(s0 + u, S - 1) * plane, lane);
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) acc.v[e] = s0 + u < S ? acc.v[e] + t[u].v[e] : acc.v[e];
+    }
+    if (bias) {
+        RowVec<EPL> bb;
+        bb.load(bias, lane);
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc.v[e] += bb.v[e];
+    }
+    RowVec<EPL> r;
+    r.load(x + (long)row * H, lane);
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) r.v[e] += acc.v[e];
+    r.store(x + (long)row * H, lane);
+    r.layer_norm(w, b, eps, lane);
+    r.store_bf16(out + (long)row * H, lane);
+}
+
 template <int EPL>
 __global__ __launch_bounds__(256) void final_norm_kernel(float* __restrict__ x, int rows, const float* __restrict__ fw,
                                                          const float* __restrict__ type_emb,
@@ -206,6 +247,18 @@ void launch_layer_norm(const float* x, int rows, const float* w, const float* b,
     if (rows <= 0) return;
     dispatch_hidden(hidden, [&]<int EPL>() {
         JH_LAUNCH(layer_norm_kernel<EPL>, row_grid(rows), dim3(256), 0, s, x, rows, w, b, eps, out);
+    });
+    HIP_CHECK(hipGetLastError());
+}
+
+void launch_resid_reduce_ln(const float* partial, int splits, int rows, int hidden, const float* bias, float* x,
+                            const float* w, const float* b, float eps, bf16_t* out, hipStream_t s) {
+    if (rows <= 0) return;
+    if (splits < 1) throw jh_error(1, "resid_reduce_ln: splits >= 1");
+    const long plane = (long)rows * hidden;
+    dispatch_hidden(hidden, [&]<int EPL>() {
+        JH_LAUNCH(resid_reduce_ln_kernel<EPL>, row_grid(rows), dim3(256), 0, s, partial, splits, plane, bias, x, rows,
+                  w, b, eps, out);
     });
     HIP_CHECK(hipGetLastError());
 }
