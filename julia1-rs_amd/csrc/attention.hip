@@ -17,12 +17,17 @@
 // already holds (the MFMA's K order is a permutation of keys; Vᵀ is read in
 // the same permutation).  P therefore never leaves registers.
 //
-// K tiles (64 keys x 64 dims) are staged row-major in LDS (stride 72 bf16:
-// conflict-free 16-byte fragment reads); V tiles are staged transposed
-// (Vᵀ[dim][key], stride 68 bf16: conflict-free 8-byte reads), both double
-// buffered with register prefetch.  Sliding-window tiles only visit keys in
-// [q_pos - window, q_pos + nq - 1 + window] ∩ [0, kv_len), with per-element
-// masking of |q - k| <= window inside the band.
+// K and V tiles (64 keys x 64 dims) reach LDS by buffer DMA, row-major with
+// 128-byte key rows and XOR-swizzled 16-byte chunks, double buffered (the DMA
+// of tile it+1 runs under the math of tile it).  K fragments are 16-byte
+// reads of key rows.  The Vᵀ fragments of Oᵀ = Vᵀ·Pᵀ come from gfx950's
+// transposing LDS read ds_read_b64_tr_b16 (measured lane layout: in each
+// group of 16 lanes, output lane i, element k' is element i%4 of the 4
+// bf16 that source lane 4k' + i/4 addresses): source lane j pointing at
+// V[kb + j/4][d0 + 4(j%4)] gives output lane i the 4 keys kb..kb+3 of dim
+// d0 + i.  No register staging or VALU transpose of V remains.
+// Sliding-window tiles only visit keys in [q_pos - window, q_pos + nq - 1 +
+// window] ∩ [0, kv_len), with per-element masking of |q - k| <= window.
 #include <hip/hip_runtime.h>
 
 #include "kernels.hpp"
@@ -30,17 +35,22 @@
 namespace {
 
 constexpr int KT = 64;       // keys per LDS tile
-constexpr int KSTR = 72;     // K tile row stride (bf16)
-constexpr int VSTR = 68;     // Vᵀ tile row stride (bf16)
 constexpr int NTHR = 256;   // four waves
 
-__global__ __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(3))) void attention_kernel(AttnArgs a) {
-    __shared__ __align__(16) bf16_t sK[2][KT][KSTR];
-    __shared__ __align__(16) bf16_t sV[2][64][VSTR];
+// Chunk swizzles of the 128-byte key rows.  K: 32 consecutive rows read one
+// 16-byte chunk each (as the GEMM operands).  V: a half-wave's transposing
+// reads touch 4 consecutive rows x 4 chunks; rows r and r+2 share a bank half,
+// so their chunks are moved 4 apart.
+__device__ constexpr int kswz(int r) { return (r >> 1) & 7; }
+__device__ constexpr int vswz(int r) { return ((r >> 1) & 1) << 2; }
+
+__global__ __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(4))) void attention_kernel(AttnArgs a) {
+    __shared__ __align__(1024) bf16_t sK[2][KT * 64];
+    __shared__ __align__(1024) bf16_t sV[2][KT * 64];
 
     const AttnTile tile = a.tiles[blockIdx.x];
     const int head = blockIdx.y;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lq = lane & 31, g = lane >> 5;
 
     const bf16_t* kbase = a.k + (long)tile.kv_row * a.ldkv + head * 64;
@@ -66,47 +76,33 @@ __global__ __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(3))) void 
         kend = min(tile.kv_len, tile.q_pos + tile.nq + a.window);
     }
 
-    // Global->register staging of one K/V tile: K as 4 16-byte chunks per
-    // thread; V as 2 (key pair x 8 dims) units per thread.
-    constexpr int KCH = KT * 8 / NTHR;   // 16-byte K chunks per thread
-    constexpr int VUN = KT * 4 / NTHR;   // (key pair, 8 dims) V units per thread
-    u32x4 rk[KCH], rv[VUN][2];
-    // Rows past the sequence end are clamped onto its last key, so every load
-    // is unconditional (a branch around a load makes the compiler wait for all
-    // loads in flight); those keys are masked to -inf before the softmax, and
-    // their V rows are finite, so they contribute exactly 0.
-    auto gload = [&](int k0) {
+    // DMA of one K/V tile into buffer `buf`: wave w fills rows [16w, 16w+16)
+    // of both with two 1 KB instructions each; lane i of instruction j takes
+    // row 16w + 8j + i/8, physical slot i%8.  Rows past the sequence end are
+    // clamped onto its last key (masked to -inf before the softmax; their
+    // finite V rows then contribute exactly 0).
+    const i32x4 rsk = make_rsrc(kbase, ((uint64_t)(tile.kv_len - 1) * a.ldkv + 64) * 2);
+    const i32x4 rsv = make_rsrc(vbase, ((uint64_t)(tile.kv_len - 1) * a.ldkv + 64) * 2);
+    const uint32_t lk0 = (uint32_t)(uintptr_t)&sK[0][0], lv0 = (uint32_t)(uintptr_t)&sV[0][0];
+    auto issue = [&](int k0, int buf) {
 #pragma unroll
-        for (int i = 0; i < KCH; ++i) {
-            int c = tid + NTHR * i, key = min(k0 + (c >> 3), kend - 1), dc = c & 7;
-            rk[i] = *(const u32x4*)(kbase + (long)key * a.ldkv + dc * 8);
-        }
-#pragma unroll
-        for (int i = 0; i < VUN; ++i) {
-            int u = tid + NTHR * i, pr = u & 31, dc = u >> 5;
-            int key = k0 + 2 * pr;
-            rv[i][0] = *(const u32x4*)(vbase + (long)min(key, kend - 1) * a.ldkv + dc * 8);
-            rv[i][1] = *(const u32x4*)(vbase + (long)min(key + 1, kend - 1) * a.ldkv + dc * 8);
+        for (int j = 0; j < 2; ++j) {
+            const int r0 = 16 * wave + 8 * j, row = r0 + (lane >> 3);
+            const int key = min(k0 + row, kend - 1);
+            const uint32_t lk = __builtin_amdgcn_readfirstlane(lk0 + (buf * KT * 64 + r0 * 64) * 2);
+            const uint32_t lv = __builtin_amdgcn_readfirstlane(lv0 + (buf * KT * 64 + r0 * 64) * 2);
+            const uint32_t ok = (uint32_t)(key * a.ldkv + (((lane & 7) ^ kswz(row)) * 8)) * 2;
+            const uint32_t ov = (uint32_t)(key * a.ldkv + (((lane & 7) ^ vswz(row)) * 8)) * 2;
+            asm volatile("buffer_load_dwordx4 %1, %2, 0 offen lds" ::"{m0}"(lk), "v"(ok), "s"(rsk) : "memory");
+            asm volatile("buffer_load_dwordx4 %1, %2, 0 offen lds" ::"{m0}"(lv), "v"(ov), "s"(rsv) : "memory");
         }
     };
-    auto sstore = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < KCH; ++i) {
-            int c = tid + NTHR * i;
-            *(u32x4*)&sK[buf][c >> 3][(c & 7) * 8] = rk[i];
-        }
-#pragma unroll
-        for (int i = 0; i < VUN; ++i) {
-            int u = tid + NTHR * i, pr = u & 31, dc = u >> 5;
-#pragma unroll
-            for (int w = 0; w < 4; ++w) {
-                uint32_t a0 = rv[i][0][w], a1 = rv[i][1][w];
-                // dims dc*8 + 2w (low halves) and dc*8 + 2w + 1 (high halves); keys 2pr, 2pr+1
-                *(uint32_t*)&sV[buf][dc * 8 + 2 * w][2 * pr] = (a0 & 0xffffu) | (a1 << 16);
-                *(uint32_t*)&sV[buf][dc * 8 + 2 * w + 1][2 * pr] = (a0 >> 16) | (a1 & 0xffff0000u);
-            }
-        }
-    };
+    // Transposing V reads: this lane's 16-lane group G and index j select
+    // key row offset 4(G/2) + j/4 and dims 16(G%2) + 4(j%4) .. +3.
+    const int tg = lane >> 4, tj = lane & 15;
+    const int vrow = 4 * (tg >> 1) + (tj >> 2);  // + 32kb + 16hb + 8·half
+    const int vch = 2 * (tg & 1) + ((tj & 3) >> 1);  // + 4db (16-byte chunk within the 64-dim row)
+    const uint32_t vhalf = (tj & 1) * 8;
 
     f32x16 o[2];
 #pragma unroll
@@ -119,24 +115,20 @@ __global__ __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(3))) void 
     const int qlo = tile.q_pos + wave * 32;
 
     const int ntk = kend > kbeg ? (kend - kbeg + KT - 1) / KT : 0;
-    if (ntk > 0) {
-        gload(kbeg);
-        sstore(0);
-    }
-    __syncthreads();
+    if (ntk > 0) issue(kbeg, 0);
     // A wave with no queries in the tile, or whose 32 queries are all outside
     // the window of a key tile, skips that tile's math (uniform per wave); it
     // still stages its share of K/V and meets every barrier.
     const bool active = wave * 32 < tile.nq;
     for (int it = 0; it < ntk; ++it) {
         const int buf = it & 1, k0 = kbeg + it * KT;
-        if (it + 1 < ntk) gload(k0 + KT);
+        // tile it landed (this wave's DMA, then everyone's), and every wave is
+        // done with tile it-1, whose buffer the next DMA refills
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (it + 1 < ntk) issue(k0 + KT, buf ^ 1);
         const bool skip = !active || (a.window >= 0 && (k0 > qlo + 31 + a.window || k0 + KT - 1 < qlo - a.window));
-        if (skip) {
-            if (it + 1 < ntk) sstore(buf ^ 1);
-            __syncthreads();
-            continue;
-        }
+        if (skip) continue;
 
         // Sᵀ for keys [k0, k0+64): two 32-key blocks.
         f32x16 s[2];
@@ -146,7 +138,8 @@ __global__ __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(3))) void 
             for (int e = 0; e < 16; ++e) s[kb][e] = 0.0f;
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
-                bf16x8 kf = *(const bf16x8*)&sK[buf][kb * 32 + lq][ks * 16 + g * 8];
+                const int r = kb * 32 + lq;
+                bf16x8 kf = *(const bf16x8*)&sK[buf][r * 64 + (((ks * 2 + g) ^ kswz(r)) * 8)];
                 s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], s[kb], 0, 0, 0);
             }
         }
@@ -218,18 +211,21 @@ __global__ __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(3))) void 
                     for (int w = 0; w < 4; ++w) r[w] = pack2(s[kb][hb * 8 + 2 * w], s[kb][hb * 8 + 2 * w + 1]);
                     pf = __builtin_bit_cast(bf16x8, r);
                 }
-                const int base = kb * 32 + hb * 16 + g * 4;
 #pragma unroll
                 for (int db = 0; db < 2; ++db) {
-                    const bf16_t* vr = &sV[buf][db * 32 + lq][0];
-                    u32x2 lo = *(const u32x2*)(vr + base);
-                    u32x2 hi = *(const u32x2*)(vr + base + 8);
+                    // keys kb*32 + hb*16 + 4g + (0..3) and + 8 + (0..3) of dim db*32 + lq
+                    u32x2 lo, hi;
+                    const int r = kb * 32 + hb * 16 + vrow;
+                    // row r + 8 has the same swizzle as row r (vswz depends on bit 1 only)
+                    const uint32_t alo = lv0 + (buf * KT * 64 + r * 64) * 2 + ((4 * db + vch) ^ vswz(r)) * 16 + vhalf;
+                    asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(lo) : "v"(alo));
+                    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:1024" : "=v"(hi) : "v"(alo));
+                    // the wait names lo/hi so no use of them is scheduled above it
+                    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(lo), "+v"(hi)::"memory");
                     bf16x8 vf = __builtin_bit_cast(bf16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
                     o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, o[db], 0, 0, 0);
                 }
             }
-        if (it + 1 < ntk) sstore(buf ^ 1);
-        __syncthreads();
     }
 
     l += __shfl_xor(l, 32, 64);

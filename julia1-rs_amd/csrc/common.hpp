@@ -55,6 +55,14 @@ __device__ inline uint32_t pack2(float a, float b) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
 }
 
+// Raw buffer resource (stride 0, 32-bit data format) over [base, base + bytes),
+// for buffer_load ... lds operand DMA.
+__device__ inline i32x4 make_rsrc(const void* base, uint64_t bytes) {
+    const uint64_t p = (uint64_t)(uintptr_t)base;
+    return i32x4{(int)(uint32_t)p, (int)(uint32_t)(p >> 32),
+                 (int)(uint32_t)(bytes < 0xffffffffull ? bytes : 0xffffffffull), 0x00020000};
+}
+
 __device__ inline float wave_sum(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, JH_WAVE);

@@ -156,13 +156,6 @@ __device__ inline void epilogue(const GemmArgs& a, f32x16 (&acc)[2][2], int fw0,
     }
 }
 
-// Raw buffer resource (stride 0, 32-bit data format) over [base, base + bytes).
-__device__ inline i32x4 make_rsrc(const void* base, uint64_t bytes) {
-    const uint64_t p = (uint64_t)(uintptr_t)base;
-    return i32x4{(int)(uint32_t)p, (int)(uint32_t)(p >> 32), (int)(uint32_t)min(bytes, (uint64_t)0xffffffffu),
-                 0x00020000};
-}
-
 // Operands reach LDS by DMA: buffer_load_dwordx4 ... lds (global_load_lds_dwordx4
 // with 64-bit per-lane addresses for row-gathered X) writes 64 lanes x 16 B to
 // one contiguous 1 KB LDS block at M0 (lane i at +16i, verified on gfx950).
