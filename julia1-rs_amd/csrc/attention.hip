@@ -99,10 +99,14 @@ __global__ __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(4))) void 
     };
     // Transposing V reads: this lane's 16-lane group G and index j select
     // key row offset 4(G/2) + j/4 and dims 16(G%2) + 4(j%4) .. +3.
+    // The row's swizzle vswz(row) equals vswz(vrow) (32kb + 16hb + 8·half keep
+    // bit 1), so per dim block db the lane's byte offset inside a tile is fixed;
+    // kb, hb and the +8-key half become immediate offsets.
     const int tg = lane >> 4, tj = lane & 15;
     const int vrow = 4 * (tg >> 1) + (tj >> 2);  // + 32kb + 16hb + 8·half
     const int vch = 2 * (tg & 1) + ((tj & 3) >> 1);  // + 4db (16-byte chunk within the 64-dim row)
-    const uint32_t vhalf = (tj & 1) * 8;
+    const uint32_t voff0 = vrow * 128 + ((vch) ^ vswz(vrow)) * 16 + (tj & 1) * 8;
+    const uint32_t voff1 = vrow * 128 + ((4 + vch) ^ vswz(vrow)) * 16 + (tj & 1) * 8;
 
     f32x16 o[2];
 #pragma unroll
@@ -129,6 +133,7 @@ __global__ __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(4))) void 
         if (it + 1 < ntk) issue(k0 + KT, buf ^ 1);
         const bool skip = !active || (a.window >= 0 && (k0 > qlo + 31 + a.window || k0 + KT - 1 < qlo - a.window));
         if (skip) continue;
+        const uint32_t vtile = lv0 + buf * KT * 64 * 2;  // this tile's V buffer (bytes)
 
         // Sᵀ for keys [k0, k0+64): two 32-key blocks.
         f32x16 s[2];
@@ -215,11 +220,20 @@ __global__ __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(4))) void 
                 for (int db = 0; db < 2; ++db) {
                     // keys kb*32 + hb*16 + 4g + (0..3) and + 8 + (0..3) of dim db*32 + lq
                     u32x2 lo, hi;
-                    const int r = kb * 32 + hb * 16 + vrow;
-                    // row r + 8 has the same swizzle as row r (vswz depends on bit 1 only)
-                    const uint32_t alo = lv0 + (buf * KT * 64 + r * 64) * 2 + ((4 * db + vch) ^ vswz(r)) * 16 + vhalf;
-                    asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(lo) : "v"(alo));
-                    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:1024" : "=v"(hi) : "v"(alo));
+                    const uint32_t base = vtile + (db ? voff1 : voff0);
+                    if (kb == 0 && hb == 0) {
+                        asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(lo) : "v"(base));
+                        asm volatile("ds_read_b64_tr_b16 %0, %1 offset:1024" : "=v"(hi) : "v"(base));
+                    } else if (kb == 0) {
+                        asm volatile("ds_read_b64_tr_b16 %0, %1 offset:2048" : "=v"(lo) : "v"(base));
+                        asm volatile("ds_read_b64_tr_b16 %0, %1 offset:3072" : "=v"(hi) : "v"(base));
+                    } else if (hb == 0) {
+                        asm volatile("ds_read_b64_tr_b16 %0, %1 offset:4096" : "=v"(lo) : "v"(base));
+                        asm volatile("ds_read_b64_tr_b16 %0, %1 offset:5120" : "=v"(hi) : "v"(base));
+                    } else {
+                        asm volatile("ds_read_b64_tr_b16 %0, %1 offset:6144" : "=v"(lo) : "v"(base));
+                        asm volatile("ds_read_b64_tr_b16 %0, %1 offset:7168" : "=v"(hi) : "v"(base));
+                    }
                     // the wait names lo/hi so no use of them is scheduled above it
                     asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(lo), "+v"(hi)::"memory");
                     bf16x8 vf = __builtin_bit_cast(bf16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
