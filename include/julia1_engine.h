@@ -13,6 +13,13 @@
  * (`Encoder`, src/encode.rs) is not part of this library: callers pass
  * token ids and marker positions, as `logits_encoded` receives them.
  *
+ * Checkpoints: julia_config.json's weight_dtype "float32" (the reference's
+ * only format: every tensor F32) or "bfloat16" (an extension: any tensor may
+ * be BF16; BF16 matrices give the same device weights as the F32 checkpoint
+ * they were rounded from, since the backend rounds F32 matrices to BF16 with
+ * the same round-to-nearest-even).  A tensor's byte length must match its
+ * shape.
+ *
  * Errors: nonzero JH_ERR_* codes with the message in jh_last_error(); the
  * messages follow the reference's wording.
  */
@@ -79,7 +86,8 @@ void je_destroy(je_engine* engine);
  * Host-only checkpoint validation, no device needed: runs the config parser,
  * the safetensors reader and the tensor-name/shape resolution of je_load and
  * writes a one-line JSON summary ({"hidden":..,"layers":..,"tensors":..,
- * "bytes":..}) into `summary` (NUL-terminated, truncated to `capacity`).
+ * "bf16_tensors":..,"bytes":..}) into `summary` (NUL-terminated, truncated to
+ * `capacity`).
  */
 int je_inspect(const char* checkpoint_dir, char* summary, size_t capacity);
 

@@ -59,6 +59,9 @@ struct ModelConfig {
     std::vector<float> rope_theta;
     float norm_eps = 1e-5f;
     uint32_t vocab = 0, max_positions = 0, head_layers = 0, head_heads = 0, head_ff = 0;
+    // weight_dtype "bfloat16": tensors may be stored as BF16 (an extension; the
+    // reference reads "float32" checkpoints only).
+    bool bf16_checkpoint = false;
 
     jh_config view() const {
         return jh_config{hidden, heads, head_dim, intermediate, layers, global.data(), half_window,
@@ -79,7 +82,9 @@ ModelConfig config_from_values(const Json& julia, const Json& enc) {
     const Json* fv = julia.get("format_version");
     if (!fv || !fv->is_uint() || fv->num != 1.0) invalid("Unsupported Julia checkpoint format");
     const Json* wd = julia.get("weight_dtype");  // absent or not a string reads as "float32"
-    if (wd && wd->kind == Json::String && wd->str != "float32") invalid("Only float32 Julia checkpoints are supported");
+    const bool bf16 = wd && wd->kind == Json::String && wd->str == "bfloat16";
+    if (wd && wd->kind == Json::String && wd->str != "float32" && !bf16)
+        invalid("Only float32 Julia checkpoints are supported");
     if (!json_eq_str(enc.get("model_type"), "modernbert")) invalid("Encoder must be ModernBERT");
     for (const char* key : {"attention_bias", "mlp_bias", "norm_bias"}) {
         const Json* v = enc.get(key);
@@ -87,6 +92,7 @@ ModelConfig config_from_values(const Json& julia, const Json& enc) {
     }
     if (!json_eq_str(enc.get("hidden_activation"), "gelu")) invalid("Unsupported encoder activation");
     ModelConfig c;
+    c.bf16_checkpoint = bf16;
     c.hidden = usize_of(enc, "hidden_size");
     c.heads = usize_of(enc, "num_attention_heads");
     c.layers = usize_of(enc, "num_hidden_layers");
@@ -139,7 +145,9 @@ ModelConfig load_config(const std::string& root) {
 // ------------------------------------------------------------ SafeTensors (src/weights.rs:32-94)
 class SafeTensors {
 public:
-    explicit SafeTensors(const std::string& path) {
+    // allow_bf16: BF16 tensors are accepted next to F32 ones and widened to
+    // FP32 on access (exact: a BF16 value is the top half of its FP32 bits).
+    SafeTensors(const std::string& path, bool allow_bf16) : allow_bf16_(allow_bf16) {
         int fd = ::open(path.c_str(), O_RDONLY);
         if (fd < 0) invalid("opening " + path + ": cannot open");
         struct stat st;
@@ -171,19 +179,37 @@ public:
     SafeTensors(const SafeTensors&) = delete;
     SafeTensors& operator=(const SafeTensors&) = delete;
 
-    // Borrowed when 4-byte aligned (the usual case), copied otherwise.
+    // F32: borrowed when 4-byte aligned (the usual case), copied otherwise.
+    // BF16: widened into an owned FP32 copy.
     const float* f32(const std::string& name, std::initializer_list<size_t> shape) {
         auto it = std::find_if(tensors_.begin(), tensors_.end(), [&](const Entry& e) { return e.name == name; });
         if (it == tensors_.end()) invalid("missing tensor " + name);
         if (!std::equal(shape.begin(), shape.end(), it->shape.begin(), it->shape.end()))
             invalid(name + ": expected shape " + fmt(std::vector<size_t>(shape)) + ", found " + fmt(it->shape));
+        size_t elems = 1;
+        for (size_t d : shape) elems *= d;
+        const size_t esize = it->bf16 ? 2 : 4;
+        if (it->end - it->begin != elems * esize) invalid(name + ": data length does not match its shape");
         const uint8_t* p = base_ + it->begin;
-        if (((uintptr_t)p & 3) == 0) return (const float*)p;
-        copies_.emplace_back((it->end - it->begin) / 4);
-        std::memcpy(copies_.back().data(), p, it->end - it->begin);
-        return copies_.back().data();
+        if (!it->bf16 && ((uintptr_t)p & 3) == 0) return (const float*)p;
+        copies_.emplace_back(elems);
+        float* dst = copies_.back().data();
+        if (!it->bf16) {
+            std::memcpy(dst, p, elems * 4);
+        } else {
+            for (size_t j = 0; j < elems; ++j) {
+                uint16_t b;
+                std::memcpy(&b, p + 2 * j, 2);
+                const uint32_t u = (uint32_t)b << 16;
+                std::memcpy(dst + j, &u, 4);
+            }
+        }
+        return dst;
     }
     size_t count() const { return tensors_.size(); }
+    size_t bf16_count() const {
+        return (size_t)std::count_if(tensors_.begin(), tensors_.end(), [](const Entry& e) { return e.bf16; });
+    }
     size_t bytes() const { return size_; }
 
 private:
@@ -191,7 +217,9 @@ private:
         std::string name;
         std::vector<size_t> shape;
         size_t begin, end;
+        bool bf16;
     };
+    bool allow_bf16_;
     const uint8_t* base_ = nullptr;
     size_t size_ = 0;
     std::vector<Entry> tensors_;
@@ -221,13 +249,17 @@ private:
         for (const auto& kv : header.obj) {
             if (kv.first == "__metadata__") continue;
             const Json& info = kv.second;
-            if (!json_eq_str(info.get("dtype"), "F32")) invalid(kv.first + ": only F32 tensors are supported");
+            const bool bf16 = allow_bf16_ && json_eq_str(info.get("dtype"), "BF16");
+            if (!bf16 && !json_eq_str(info.get("dtype"), "F32"))
+                invalid(kv.first + (allow_bf16_ ? ": only F32 and BF16 tensors are supported"
+                                                : ": only F32 tensors are supported"));
             const Json* shape = info.get("shape");
             const Json* offs = info.get("data_offsets");
             if (!shape || shape->kind != Json::Array) invalid("shape");
             if (!offs || offs->kind != Json::Array || offs->arr.size() != 2) invalid("data_offsets");
             Entry e;
             e.name = kv.first;
+            e.bf16 = bf16;
             for (const Json& d : shape->arr) {
                 if (!d.is_uint()) invalid("shape");
                 e.shape.push_back((size_t)d.num);
@@ -338,12 +370,13 @@ int je_inspect(const char* dir, char* summary, size_t capacity) {
         if (!dir) invalid("null checkpoint path");
         const std::string root(dir);
         ModelConfig c = load_config(root);
-        SafeTensors t(root + "/model.safetensors");
+        SafeTensors t(root + "/model.safetensors", c.bf16_checkpoint);
         HostWeights hw = load_weights(t, c);
         (void)hw;
         std::string s = "{\"hidden\":" + std::to_string(c.hidden) + ",\"layers\":" + std::to_string(c.layers) +
                         ",\"head_layers\":" + std::to_string(c.head_layers) + ",\"tensors\":" +
-                        std::to_string(t.count()) + ",\"bytes\":" + std::to_string(t.bytes()) + "}";
+                        std::to_string(t.count()) + ",\"bf16_tensors\":" + std::to_string(t.bf16_count()) +
+                        ",\"bytes\":" + std::to_string(t.bytes()) + "}";
         if (summary && capacity) {
             size_t n = std::min(capacity - 1, s.size());
             std::memcpy(summary, s.data(), n);
@@ -367,7 +400,7 @@ int je_load(const char* dir, const je_options* options, je_engine** out) {
             invalid("max_length must be an integer between 1 and " + std::to_string(e->config.max_positions));
         if (file_exists(root + "/INCOMPLETE") || file_exists(root + "/quantization.json"))
             invalid("INT8 checkpoints are not supported by this runtime");
-        SafeTensors t(root + "/model.safetensors");
+        SafeTensors t(root + "/model.safetensors", e->config.bf16_checkpoint);
         // assemble (src/engine.rs:147-172)
         if (opts.batch_size < 1 || opts.max_batch_tokens < max_length) invalid("Invalid batch size / token budget");
         HostWeights hw = load_weights(t, e->config);

@@ -104,7 +104,7 @@ class ModelConfig:
         """Restates src/config.rs:43-96 (same checks, same derived fields)."""
         if julia.get("format_version") != 1:
             raise ValueError("Unsupported Julia checkpoint format")
-        if julia.get("weight_dtype", "float32") != "float32":
+        if julia.get("weight_dtype", "float32") not in ("float32", "bfloat16"):
             raise ValueError("Only float32 Julia checkpoints are supported")
         if enc.get("model_type") != "modernbert":
             raise ValueError("Encoder must be ModernBERT")

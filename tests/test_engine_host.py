@@ -122,3 +122,95 @@ def test_load_without_gpu_fails_cleanly(tiny_ckpt):
     with pytest.raises(hip.HipError) as e:
         engine.Engine.load(tiny_ckpt)
     assert e.value.code == 2
+
+
+def test_bf16_rounding_matches_torch():
+    """checkpoint.bf16_bits against torch's FP32 -> BF16 conversion (round to
+    nearest even), on random values and the tie/overflow/NaN special cases."""
+    torch = pytest.importorskip("torch")
+    from julia1_amd import checkpoint
+    rng = np.random.default_rng(5)
+    u = np.concatenate([rng.integers(0, 2**32, 100000, dtype=np.uint64).astype(np.uint32),
+                        np.array([0x3F808000, 0x3F818000, 0x3F807FFF, 0x7F7FFFFF, 0xFF7FFFFF, 0x7F800000,
+                                  0x00008000, 0x00018000, 0x80000000], dtype=np.uint32)])
+    a = u.view(np.float32)
+    finite = np.isfinite(a)
+    got = checkpoint.bf16_bits(a)
+    want = torch.from_numpy(a.copy()).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got[finite], want[finite])
+    assert got[-9] == 0x3F80 and got[-8] == 0x3F82 and got[-7] == 0x3F80 and got[-6] == 0x7F80
+    nan = np.isnan(a)
+    assert np.isnan(checkpoint.bf16_to_f32(got[nan])).all()
+    assert np.array_equal(checkpoint.bf16_to_f32(got[finite]).view(np.uint32),
+                          want[finite].astype(np.uint32) << np.uint32(16))
+
+
+@pytest.fixture(scope="module")
+def bf16_ckpt(tiny_ckpt, tmp_path_factory):
+    from julia1_amd import checkpoint
+    return checkpoint.convert_to_bf16(tiny_ckpt, str(tmp_path_factory.mktemp("bf16")))
+
+
+def test_bf16_checkpoint_layout(tiny_ckpt, bf16_ckpt):
+    """The converted file reads back through the safetensors library itself:
+    matrices as torch's BF16 rounding of the F32 originals, the rest unchanged."""
+    torch = pytest.importorskip("torch")
+    from safetensors.torch import load_file
+    from julia1_amd import checkpoint
+    src = load_file(os.path.join(tiny_ckpt, "model.safetensors"))
+    dst = load_file(os.path.join(bf16_ckpt, "model.safetensors"))
+    assert src.keys() == dst.keys()
+    n_bf16 = 0
+    for name, a in src.items():
+        b = dst[name]
+        if checkpoint.is_bf16_matrix(name):
+            n_bf16 += 1
+            assert b.dtype == torch.bfloat16 and torch.equal(b, a.to(torch.bfloat16))
+        else:
+            assert b.dtype == torch.float32 and torch.equal(a, b)
+    cfg = synth.model_config("tiny")
+    assert n_bf16 == 4 * cfg.layers + 4 * cfg.head_layers + 1
+    assert json.load(open(os.path.join(bf16_ckpt, "julia_config.json")))["weight_dtype"] == "bfloat16"
+    s = engine.inspect(bf16_ckpt)
+    assert s["tensors"] == len(src) and s["bf16_tensors"] == n_bf16
+    assert engine.inspect(tiny_ckpt)["bf16_tensors"] == 0
+    assert s["bytes"] < 0.75 * os.path.getsize(os.path.join(tiny_ckpt, "model.safetensors"))
+
+
+def test_bf16_checkpoint_errors(tiny_ckpt, bf16_ckpt, tmp_path):
+    from julia1_amd import checkpoint
+    # BF16 tensors under weight_dtype float32: the reference's F32-only rule.
+    d = _copy_ckpt(bf16_ckpt, str(tmp_path / "a"), julia={"weight_dtype": "float32"})
+    with pytest.raises(hip.HipError, match="only F32 tensors are supported"):
+        engine.inspect(d)
+    # bfloat16 checkpoints accept F32 and BF16, nothing else.
+    d = _copy_ckpt(tiny_ckpt, str(tmp_path / "b"), julia={"weight_dtype": "bfloat16"},
+                   weights=_safetensors({"x": np.zeros(3)}, dtype="F16"))
+    with pytest.raises(hip.HipError, match="only F32 and BF16 tensors are supported"):
+        engine.inspect(d)
+    # An all-F32 file is a valid bfloat16 checkpoint.
+    d = _copy_ckpt(tiny_ckpt, str(tmp_path / "c"), julia={"weight_dtype": "bfloat16"})
+    assert engine.inspect(d)["bf16_tensors"] == 0
+    # A tensor whose shape, or whose byte length, disagrees with what the model needs.
+    cfg = synth.model_config("tiny")
+    t = synth.make_weights(cfg, seed=3)
+    name = "encoder.layers.0.attn.Wo.weight"
+    p = str(tmp_path / "d.safetensors")
+    checkpoint.write_safetensors(p, {k: (("BF16", checkpoint.bf16_bits(v)) if k == name else v) for k, v in t.items()})
+    blob = open(p, "rb").read()
+    n = int.from_bytes(blob[:8], "little")
+    data = blob[8 + n:]
+
+    def with_header(edit, sub):
+        header = json.loads(blob[8:8 + n])
+        edit(header[name])
+        h = json.dumps(header).encode()
+        h += b" " * (-len(h) % 8)
+        return _copy_ckpt(tiny_ckpt, str(tmp_path / sub), julia={"weight_dtype": "bfloat16"},
+                          weights=len(h).to_bytes(8, "little") + h + data)
+
+    assert engine.inspect(with_header(lambda e: None, "e"))["bf16_tensors"] == 1
+    with pytest.raises(hip.HipError, match=r"attn.Wo.weight: expected shape \[128, 128\], found \[128, 64\]"):
+        engine.inspect(with_header(lambda e: e.update(shape=[128, 64]), "f"))
+    with pytest.raises(hip.HipError, match="attn.Wo.weight: data length does not match its shape"):
+        engine.inspect(with_header(lambda e: e.update(data_offsets=[e["data_offsets"][0], e["data_offsets"][1] - 2]), "g"))

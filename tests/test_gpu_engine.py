@@ -55,3 +55,23 @@ def test_engine_rejects_rows_over_max_length(setup):
     with pytest.raises(hip.HipError, match="longer than max_length"):
         e.logits_encoded([(np.zeros(65, dtype=np.uint32), [0], 0)])
     assert e.logits_encoded([]) == []
+
+
+def test_bf16_checkpoint_gives_identical_logits(setup, tmp_path):
+    """A weight_dtype "bfloat16" checkpoint (matrices stored as their BF16
+    rounding, FP32-resident tensors kept F32) loads to the same device weights
+    as the F32 checkpoint it came from: logits are bit-identical.  Rounding the
+    FP32-resident tensors too moves the logits by that rounding only."""
+    from julia1_amd import checkpoint
+    root, cfg, orc = setup
+    half = checkpoint.convert_to_bf16(root, str(tmp_path / "bf16"))
+    every = checkpoint.convert_to_bf16(root, str(tmp_path / "all"), all_tensors=True)
+    b = synth.make_batch([50, 3, 200, 17, 90, 64, 1, 130], [2, 1, 6, 3, 4, 5, 1, 20], cfg.vocab, 14)
+    items = list(b.items())
+    want = engine.Engine.load(root).logits_encoded(items)
+    got = engine.Engine.load(half).logits_encoded(items)
+    rough = engine.Engine.load(every).logits_encoded(items)
+    ref = b.split_scores(orc.forward(b))
+    for w, g, r, o in zip(want, got, rough, ref):
+        assert np.array_equal(w.view(np.uint32), g.view(np.uint32))
+        assert np.abs(r - o).max() <= 2e-2
