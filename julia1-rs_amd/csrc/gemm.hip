@@ -60,6 +60,21 @@ __device__ inline void epilogue(const GemmArgs& a, f32x16 (&acc)[2][2], int fw0,
     constexpr int CPR = OW / 4;          // 16-byte FP32 chunks per staging row
     const int g4 = (lane >> 5) * 4, lr = lane & 31;
     auto put = [&](int row, int chunk, f32x4 v) { *(f32x4*)&stage[row * OW + ((chunk ^ oswz<CPR>(row)) * 4)] = v; };
+    const long col0 = a.col + (GEGLU ? fw0 / 2 : fw0);
+
+    // Residual: all 16 of this lane's old FP32 chunks are loaded before the
+    // staging pass (rows past the end re-read the last row and are not
+    // stored), so their latency overlaps it instead of serialising the
+    // read-modify-write loop one row pass at a time.
+    constexpr int RPASS = 16;  // 4-row passes over the 64 staged rows
+    f32x4 old[EPI == JH_EPI_RESID_F32 ? RPASS : 1];
+    if constexpr (EPI == JH_EPI_RESID_F32) {
+#pragma unroll
+        for (int p = 0; p < RPASS; ++p) {
+            const int t = min(tw0 + (lane >> 4) + 4 * p, a.rows - 1);
+            old[p] = *(const f32x4*)((const float*)a.out + (long)t * a.ldo + col0 + (lane & 15) * 4);
+        }
+    }
 
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -121,23 +136,23 @@ __device__ inline void epilogue(const GemmArgs& a, f32x16 (&acc)[2][2], int fw0,
         }
     }
 
-    const long col0 = a.col + (GEGLU ? fw0 / 2 : fw0);
     if constexpr (F32OUT) {
         // 16 lanes per 256-byte row, 4 rows per pass.
         const int q = lane & 15;
-#pragma unroll 4
-        for (int rr = lane >> 4; rr < 64; rr += 4) {
-            const int t = tw0 + rr;
-            if (t >= a.rows) break;
-            const f32x4 v = *(const f32x4*)&stage[rr * OW + ((q ^ oswz<CPR>(rr)) * 4)];
-            float* o = (float*)a.out + (long)t * a.ldo + col0 + q * 4;
-            if constexpr (EPI == JH_EPI_RESID_F32) {
-                f32x4 old = *(const f32x4*)o;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) old[e] += v[e];
-                *(f32x4*)o = old;
-            } else {
-                *(f32x4*)o = v;
+        for (int p = 0; p < RPASS; ++p) {
+            const int rr = (lane >> 4) + 4 * p, t = tw0 + rr;
+            if (t < a.rows) {
+                const f32x4 v = *(const f32x4*)&stage[rr * OW + ((q ^ oswz<CPR>(rr)) * 4)];
+                float* o = (float*)a.out + (long)t * a.ldo + col0 + q * 4;
+                if constexpr (EPI == JH_EPI_RESID_F32) {
+                    f32x4 r = old[p];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) r[e] += v[e];
+                    *(f32x4*)o = r;
+                } else {
+                    *(f32x4*)o = v;
+                }
             }
         }
     } else {
@@ -172,7 +187,7 @@ __device__ inline void epilogue(const GemmArgs& a, f32x16 (&acc)[2][2], int fw0,
 // insert its conservative vmcnt(0) before every LDS read; the wait for a stage
 // is explicit.
 template <int EPI, bool GATHER>
-__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void gemm_kernel(GemmArgs a) {
     constexpr int BF = 128, BT = 128, FB = 2, TB = 2, NS = 2;
     constexpr int CPR = BK / 8;           // 16-byte chunks per row (8)
     constexpr int RPI = 64 / CPR;         // rows per 1 KB DMA instruction (8)
@@ -261,25 +276,39 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
         if (kt + 1 < KT) issue(kt + 1, st ^ 1);
         const bf16_t* W = sW + st * STAGE;
         const bf16_t* X = sX + st * STAGE;
-#pragma unroll
-        for (int ks = 0; ks < BK / 16; ++ks) {
+        // Fragments are double-buffered in registers: the LDS reads of slice
+        // ks+1 are in flight while the MFMAs of slice ks run.
+        bf16x8 af[2][FB], bx[2][TB];
+        auto load = [&](int ks, int s) {
             const int c = ks * 2 + lg;
-            bf16x8 af[FB], bx[TB];
 #pragma unroll
             for (int i = 0; i < FB; ++i) {
                 const int r = wf * 64 + i * 32 + lr;
-                af[i] = *(const bf16x8*)&W[r * BK + ((c ^ swz(r)) * 8)];
+                af[s][i] = *(const bf16x8*)&W[r * BK + ((c ^ swz(r)) * 8)];
             }
 #pragma unroll
             for (int j = 0; j < TB; ++j) {
                 const int r = wt * 64 + j * 32 + lr;
-                bx[j] = *(const bf16x8*)&X[r * BK + ((c ^ swz(r)) * 8)];
+                bx[s][j] = *(const bf16x8*)&X[r * BK + ((c ^ swz(r)) * 8)];
             }
+        };
+        // Order pinned with scheduling fences: reads of slices 0 and 1, then
+        // per slice its MFMAs followed by the reads of the slice two ahead
+        // into the registers those MFMAs just consumed (left to itself the
+        // compiler reuses one fragment set and waits out every read).
+        load(0, 0);
+        load(1, 1);
+#pragma unroll
+        for (int ks = 0; ks < BK / 16; ++ks) {
+            const int s = ks & 1;
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int i = 0; i < FB; ++i)
 #pragma unroll
                 for (int j = 0; j < TB; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bx[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[s][i], bx[s][j], acc[i][j], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            if (ks + 2 < BK / 16) load(ks + 2, s);
         }
     }
     __syncthreads();  // every wave is done reading the operand stages
@@ -390,7 +419,13 @@ __global__ __launch_bounds__(256) void splitk_reduce(GemmArgs a, int S) {
 // 512 DMA bytes per MFMA) and 256x256 (8 waves of 128x64): in the encoder
 // forward they tie at config1 and lose ~10% at M = 16384, because the two
 // independent workgroups per CU hide each other's prologue, barrier waits and
-// epilogue, which a single workgroup per CU leaves exposed.
+// epilogue, which a single workgroup per CU leaves exposed.  A 256x128 tile
+// with BK 32, three 24 KB stages and four 128x64 waves keeps two workgroups
+// per CU and moves 25% fewer bytes per MFMA (L2 -> LDS and LDS -> registers),
+// yet its K loop took as many cycles per MFMA; with the DMA spread between
+// the MFMAs it only tied.  In this kernel the shader clock runs at ~1.5-1.8
+// GHz (against ~2.2 GHz for the same MFMAs without operand traffic), i.e. the
+// GEMMs are power-limited by operand movement as much as by issue.
 // Split count for an output of `tiles` 128x128 tiles: enough workgroups to
 // cover the GPU about once (256 CUs x 2 resident) when the tile count alone
 // leaves most CUs idle, at least two 64-deep K steps per split, and the
