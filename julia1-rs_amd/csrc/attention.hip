@@ -1,10 +1,10 @@
 // FlashAttention-2 forward for gfx950: one workgroup of four waves per
 // (128-query tile, head); each wave owns 32 queries.  Four waves share every
 // staged K/Vᵀ tile (half the LDS staging per query of a 64-query tile), and
-// the register budget is held to three resident waves per SIMD so that one
-// wave's softmax VALU work (about twice its MFMA time at head_dim 64)
-// overlaps other waves' MFMAs.  Measured on MI355X at L = 8192: 1.6x the
-// throughput of two-wave workgroups at two waves per SIMD.
+// the register budget is held to four resident waves per SIMD (at most 128
+// VGPRs) so that one wave's softmax VALU work (more than its MFMA time at
+// head_dim 64) overlaps other waves' MFMAs.  Measured on MI355X at L = 8192:
+// 1.6x the throughput of two-wave workgroups at two waves per SIMD.
 //
 // The score tile is computed transposed, Sᵀ = K·Qᵀ, with
 // v_mfma_f32_32x32x16_bf16 (M = 32 keys, N = 32 queries, K = 16 head dims).
@@ -28,6 +28,13 @@
 // d0 + i.  No register staging or VALU transpose of V remains.
 // Sliding-window tiles only visit keys in [q_pos - window, q_pos + nq - 1 +
 // window] ∩ [0, kv_len), with per-element masking of |q - k| <= window.
+//
+// Per 64-key tile a wave issues 16 MFMAs (512 cycles) and ~33 quarter-rate
+// v_exp_f32 (~530 cycles) plus the rest of the softmax, so the exponentials
+// alone bound it near 50% MFMA utilisation at head_dim 64; the running max is
+// therefore only moved, and O rescaled, when it grows by more than 2^8 in p
+// (a wave-uniform branch), which removes most of the 32 rescale multiplies
+// per tile.
 #include <hip/hip_runtime.h>
 
 #include "kernels.hpp"
@@ -115,6 +122,7 @@ __global__ __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(4))) void 
     // evaluated as one FMA per score; m is the running max of the raw scores.
     float m = -INFINITY, l = 0.0f;
     const float c = a.scale_log2;
+    const float thr = 8.0f / c;  // raw-score growth of the max that forces a rescale
     // Queries of this wave sit at positions [qlo, qlo + 31].
     const int qlo = tile.q_pos + wave * 32;
 
@@ -181,8 +189,12 @@ __global__ __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(4))) void 
 #pragma unroll
             for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[kb][e]);
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float mn = fmaxf(m, mx);
-        {  // rescale unconditionally: straight-line code keeps O in place
+        // Lazy rescale: the running max moves (and O, l are rescaled) only
+        // when some lane's tile max exceeds it by more than 2^8 in p; the
+        // branch is wave-uniform.  Until then p may reach 2^8, which bf16 P
+        // and the FP32 sums carry without loss of relative precision.
+        if (__builtin_amdgcn_ballot_w64(mx > m + thr) != 0) {
+            const float mn = fmaxf(m, mx);
             const float alpha = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m - mn) * c);
             l *= alpha;
 #pragma unroll
