@@ -88,6 +88,69 @@ def kernel_table(stats, steps):
     return out
 
 
+# The reference's published CUDA figures (README:168-200, bench/results/final.jsonl:2): Julia-1 on an RTX 4090,
+# tokenization included, through Engine::predict with batch_size 16 (src/bin/julia1.rs:244-319).
+REFERENCE_CUDA = {"single_mean_ms": 0.934, "single_p50_ms": 0.920, "single_p99_ms": 1.035, "batch_rows_per_s": 3202.4,
+                  "long_best_ms": {"933": 1.998, "3928": 7.479, "7556": 20.506}, "hardware": "RTX 4090"}
+
+
+def reference_protocol(np, synth, engine):
+    """The reference's own bench protocol (src/bin/julia1.rs:244-319) on its own model shape ("julia1": hidden 384,
+    22 layers), through the C++ engine (Engine::logits_encoded with length-sorted micro-batches of 16 rows).
+
+    Rows are synthetic: single requests ~U[140,180] tokens (the published ~160), the 2000-row batch
+    ~U[32,554] (the published mean of ~293 tokens per row), 2-8 options per row, long requests of 933, 3928
+    and 7556 tokens with 4 options. Tokenization is not part of these timings (there is no tokenizer here);
+    it is part of the reference's."""
+    import shutil
+    import tempfile
+    cfg = synth.model_config("julia1")
+    root = tempfile.mkdtemp(prefix="julia1_ckpt_")
+    try:
+        synth.write_checkpoint(root, "julia1", synth.make_weights(cfg, seed=0))
+        e = engine.Engine.load(root, "hip:0", batch_size=16, max_batch_tokens=65536)
+    finally:
+        shutil.rmtree(root, ignore_errors=True)
+    rng = np.random.default_rng(7)
+
+    def rows(n, lo, hi, seed):
+        lens = rng.integers(lo, hi + 1, n)
+        return list(synth.make_batch(lens, rng.integers(2, 9, n), cfg.vocab, seed).items())
+
+    singles, batch = rows(520, 140, 180, 11), rows(2000, 32, 554, 12)
+    longs = {n: list(synth.make_batch([n], [4], cfg.vocab, n).items()) for n in (933, 3928, 7556)}
+    # warm-up as the reference does: 20 single rows, a 64-row batch, each long row once
+    for it in singles[:20]:
+        e.logits_encoded([it])
+    e.logits_encoded(batch[:64])
+    for it in longs.values():
+        e.logits_encoded(it)
+    lat = []
+    for it in singles[20:]:
+        t = time.perf_counter()
+        e.logits_encoded([it])
+        lat.append((time.perf_counter() - t) * 1e3)
+    lat.sort()
+    best = min(_timed(lambda: e.logits_encoded(batch)) for _ in range(3))
+    long_ms = {str(n): round(min(_timed(lambda: e.logits_encoded(it)) for _ in range(3)) * 1e3, 3)
+               for n, it in longs.items()}
+    out = dict(shape="julia1: hidden 384, 6x64 heads, GEGLU 1152, 22 layers, 2 head layers (synthetic weights)",
+               single=dict(n=len(lat), mean_ms=round(float(np.mean(lat)), 3), p50_ms=round(lat[len(lat) // 2], 3),
+                           p99_ms=round(lat[int(0.99 * (len(lat) - 1))], 3)),
+               batch=dict(n=len(batch), tokens=int(sum(len(i[0]) for i in batch)), best_s=round(best, 4),
+                          rows_per_s=round(len(batch) / best, 1)),
+               long_best_ms=long_ms, reference_cuda=REFERENCE_CUDA,
+               note="tokenization excluded here, included in the reference's figures")
+    e.close()
+    return out
+
+
+def _timed(fn):
+    t = time.perf_counter()
+    fn()
+    return time.perf_counter() - t
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -258,6 +321,9 @@ def main():
                              forward_ms=round(fw, 3), forward_with_pcie_ms=round(pw, 3),
                              tokens_per_s=round(bw.tokens / fw * 1e3))
             log(f"{wl}: {bw.tokens} tokens, forward {fw:.3f} ms ({pw:.3f} ms with PCIe)")
+        from julia1_amd import engine
+        extra["reference_protocol"] = reference_protocol(np, synth, engine)
+        log("reference protocol (julia1 shape):", extra["reference_protocol"])
 
     cpu = None
     parity = None

@@ -44,15 +44,16 @@ __device__ constexpr int oswz(int r) {
     return CPR == 16 ? (r & 15) : ((r >> 1) & 7);
 }
 
-// Epilogue of one wave's 64 x 64 tile (features fw0.., tokens tw0..).
+// Epilogue of one wave's 64 x (32·TB) tile (features fw0.., tokens tw0..).
 // acc[i][j][e] holds feature fw0 + i*32 + (e/4)*8 + g4 + e%4 of token
 // tw0 + j*32 + lr.  Phase 1 applies the elementwise part in registers and
 // writes FP32 results to the wave's staging rows in LDS ([token][column]);
 // phase 2 reads them back along rows so each store instruction writes whole
 // 128/256-byte row segments (8 or 4 rows per instruction) instead of 32
 // scattered 16-byte pieces.
-template <int EPI>
-__device__ inline void epilogue(const GemmArgs& a, f32x16 (&acc)[2][2], int fw0, int tw0, int lane, float* stage) {
+template <int EPI, int TB = 2>
+__device__ inline void epilogue(const GemmArgs& a, f32x16 (&acc)[2][TB], int fw0, int tw0, int lane, float* stage) {
+    constexpr int ROWS = TB * 32;  // staged token rows
     constexpr bool GEGLU = EPI == JH_EPI_GEGLU_BF16;
     constexpr bool F32OUT = EPI == JH_EPI_RESID_F32 || EPI == JH_EPI_BIAS_F32 || EPI == EPI_PARTIAL;
     constexpr bool BIASED = EPI == JH_EPI_BIAS_BF16 || EPI == JH_EPI_BIAS_RELU_BF16 || EPI == JH_EPI_BIAS_F32;
@@ -66,7 +67,7 @@ __device__ inline void epilogue(const GemmArgs& a, f32x16 (&acc)[2][2], int fw0,
     // staging pass (rows past the end re-read the last row and are not
     // stored), so their latency overlaps it instead of serialising the
     // read-modify-write loop one row pass at a time.
-    constexpr int RPASS = 16;  // 4-row passes over the 64 staged rows
+    constexpr int RPASS = ROWS / 4;  // 4-row passes over the staged rows
     f32x4 old[EPI == JH_EPI_RESID_F32 ? RPASS : 1];
     if constexpr (EPI == JH_EPI_RESID_F32) {
 #pragma unroll
@@ -77,7 +78,7 @@ __device__ inline void epilogue(const GemmArgs& a, f32x16 (&acc)[2][2], int fw0,
     }
 
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < TB; ++j) {
         const int tl = j * 32 + lr;
         if constexpr (EPI == JH_EPI_ROPE_BF16) {
             const bool rot = fw0 < a.rope_cols;
@@ -160,7 +161,7 @@ __device__ inline void epilogue(const GemmArgs& a, f32x16 (&acc)[2][2], int fw0,
         constexpr int LPR = OW / 8, RPP = 64 / LPR;
         const int q = lane % LPR;
 #pragma unroll 4
-        for (int rr = lane / LPR; rr < 64; rr += RPP) {
+        for (int rr = lane / LPR; rr < ROWS; rr += RPP) {
             const int t = tw0 + rr;
             if (t >= a.rows) break;
             const f32x4 v0 = *(const f32x4*)&stage[rr * OW + (((2 * q) ^ oswz<CPR>(rr)) * 4)];
@@ -324,6 +325,108 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     }
 }
 
+// Small batches in one launch, without the split-K workspace or its reduce
+// kernel.  A workgroup owns a 64-feature x 32-token tile and the whole K: every
+// operand chunk reaches LDS in a single round of DMA, laid out as K/64 blocks
+// of the main kernel's stage layout (so the fragment reads are the same
+// conflict-free ones).  The four waves each multiply a quarter of the 16-deep
+// K slices; waves 1-3 hand their partial tiles to wave 0 through LDS, which
+// adds them in wave order (deterministic) and runs the epilogue.  For a
+// ~160-token request this replaces a split-K pass plus a reduce kernel
+// (two dependent launches of ~5 and ~4 us) by one launch.
+constexpr int SMALL_KMAX = 768;  // (64 + 32) rows x 768 x 2 B = 144 KB of LDS
+constexpr int SMALL_BF = 64, SMALL_BT = 32;
+
+template <int EPI, bool GATHER>
+__global__ __launch_bounds__(256) void gemm_small_kernel(GemmArgs a) {
+    constexpr int BF = SMALL_BF, BT = SMALL_BT;
+    __shared__ __align__(1024) bf16_t smem[(BF + BT) * SMALL_KMAX];
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nF = a.n / BF;
+    const int f0 = (int)(blockIdx.x % nF) * BF, t0 = (int)(blockIdx.x / nF) * BT;
+    const int nseg = a.k / 64;  // 128-byte row segments
+    bf16_t* const sW = smem;                     // segment g: rows [0, BF) at sW + g*BF*64
+    bf16_t* const sX = smem + nseg * BF * 64;    // segment g: rows [0, BT) at sX + g*BT*64
+
+    // DMA: per segment 8 instructions of 8 W rows and 4 of 8 X rows; wave w
+    // issues instructions w, w+4, ...  Rows past the end are clamped (never
+    // stored), as in gemm_kernel.
+    const bf16_t* wt0 = a.w + (long)f0 * a.k;
+    const bf16_t* xt0 = a.x + (long)t0 * a.ldx;
+    const i32x4 rw = make_rsrc(wt0, (uint64_t)(a.n - f0) * a.k * 2);
+    const i32x4 rx = make_rsrc(xt0, (uint64_t)(a.rows - 1 - t0) * a.ldx * 2 + (uint64_t)a.k * 2);
+    const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
+    for (int i = wave; i < 12 * nseg; i += 4) {
+        const int g = i / 12, j = i - g * 12;  // wave-uniform
+        const int row = (j < 8 ? j : j - 8) * 8 + (lane >> 3);
+        const int c = (lane & 7) ^ ((row >> 1) & 7);
+        const uint32_t kb = (uint32_t)g * 128;
+        if (j < 8) {
+            const uint32_t l = __builtin_amdgcn_readfirstlane(lds0 + (uint32_t)((g * BF + j * 8) * 64) * 2);
+            const uint32_t off = (uint32_t)((min(f0 + row, a.n - 1) - f0) * a.k + c * 8) * 2;
+            asm volatile("buffer_load_dwordx4 %1, %2, %3 offen lds" ::"{m0}"(l), "v"(off), "s"(rw), "s"(kb) : "memory");
+        } else {
+            const uint32_t l = __builtin_amdgcn_readfirstlane(
+                lds0 + (uint32_t)((nseg * BF * 64 + (g * BT + (j - 8) * 8) * 64) * 2));
+            const int t = min(t0 + row, a.rows - 1);
+            if constexpr (GATHER) {
+                const bf16_t* src = a.x + (long)a.gather[t] * a.ldx + g * 64 + c * 8;
+                asm volatile("global_load_lds_dwordx4 %1, off" ::"{m0}"(l), "v"(src) : "memory");
+            } else {
+                const uint32_t off = (uint32_t)((t - t0) * (long)a.ldx + c * 8) * 2;
+                asm volatile("buffer_load_dwordx4 %1, %2, %3 offen lds" ::"{m0}"(l), "v"(off), "s"(rx), "s"(kb)
+                             : "memory");
+            }
+        }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+
+    // This wave's quarter of the K/16 slices: slice s lies in segment s/4 at
+    // chunk pair 2(s%4) + (lane >= 32).
+    const int lr = lane & 31, lg = lane >> 5;
+    f32x16 acc[2][1];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[i][0][e] = 0.0f;
+    const int nsl = a.k / 16, s0 = wave * (nsl / 4), s1 = s0 + nsl / 4;
+    for (int sl = s0; sl < s1; ++sl) {
+        const int g = sl >> 2, c = (sl & 3) * 2 + lg;
+        const bf16x8 bx = *(const bf16x8*)&sX[g * BT * 64 + lr * 64 + ((c ^ ((lr >> 1) & 7)) * 8)];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int r = i * 32 + lr;
+            const bf16x8 af = *(const bf16x8*)&sW[g * BF * 64 + r * 64 + ((c ^ ((r >> 1) & 7)) * 8)];
+            acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, bx, acc[i][0], 0, 0, 0);
+        }
+    }
+    __syncthreads();  // operand LDS is free: reused for the partial tiles and the staging rows
+    // Partial tile of wave w (1..3): 8 blocks of 64 lanes x 16 B, element e of
+    // block q is acc[q/4][0][4(q%4) + e].
+    float* const red = (float*)smem;
+    if (wave > 0) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            f32x4 v;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = acc[q >> 2][0][(q & 3) * 4 + e];
+            *(f32x4*)&red[(((wave - 1) * 8 + q) * 64 + lane) * 4] = v;
+        }
+    }
+    __syncthreads();
+    if (wave > 0) return;
+#pragma unroll
+    for (int w = 0; w < 3; ++w)
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const f32x4 v = *(const f32x4*)&red[((w * 8 + q) * 64 + lane) * 4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[q >> 2][0][(q & 3) * 4 + e] += v[e];
+        }
+    epilogue<EPI, 1>(a, acc, f0, t0, lane, red + 3 * 8 * 64 * 4);
+}
+
 // Split-K reduction + epilogue: thread (row t, 64-wide slab, q) sums the S
 // partials of columns slab + 4q .. +3 and slab + 32 + 4q .. +3 in split order
 // and applies the same elementwise epilogue, with the same expression order,
@@ -441,10 +544,23 @@ int splitk_count(const GemmArgs& a, long tiles) {
     return (kt + chunk - 1) / chunk;
 }
 
+// The one-launch small-batch kernel replaces split-K where split-K would run
+// automatically (workspace given, no forced split count) and K fits its LDS.
+bool use_small(const GemmArgs& a, long tiles) {
+    return a.partial && a.splits == 0 && a.k <= SMALL_KMAX && splitk_count(a, tiles) > 1;
+}
+
 template <int EPI>
 void launch_cfg(const GemmArgs& a, hipStream_t s) {
     constexpr int BF = 128, BT = 128;
     const int blocks = ((a.n + BF - 1) / BF) * ((a.rows + BT - 1) / BT);
+    if (use_small(a, blocks)) {
+        const int sblocks = (a.n / SMALL_BF) * ((a.rows + SMALL_BT - 1) / SMALL_BT);
+        if (a.gather) JH_LAUNCH((gemm_small_kernel<EPI, true>), dim3(sblocks), dim3(256), 0, s, a);
+        else JH_LAUNCH((gemm_small_kernel<EPI, false>), dim3(sblocks), dim3(256), 0, s, a);
+        HIP_CHECK(hipGetLastError());
+        return;
+    }
     const int S = splitk_count(a, blocks);
     if (S > 1) {
         GemmArgs p = a;

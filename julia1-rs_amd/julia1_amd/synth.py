@@ -36,11 +36,15 @@ def julia_config(head_layers=2):
     return {"format_version": 1, "weight_dtype": "float32", "head_layers": head_layers}
 
 
-# Named model shapes.  "modernbert-base" is the BASELINE shape; "julia1-384" is
-# the hidden-384 shape of the reference's own CUDA path; "tiny" is small enough
-# for f64 cross-checks.
+# Named model shapes.  "modernbert-base" is the BASELINE shape.  "julia1" is
+# the reference's own model as its CUDA path and tests describe it: hidden 384
+# (src/cuda/mod.rs:175), Wqkv [1152, 384], Wi [2304, 384] and Wo [384, 1152]
+# (src/cpu/gemm.rs:380-438), 22 layers (README:212); the head-layer count is
+# not published and is taken as 2.  "julia1-384" is a 6-layer cut of the
+# hidden-384 shape for quick tests; "tiny" is small enough for f64 cross-checks.
 SHAPES = {
     "modernbert-base": dict(enc=encoder_config(), julia=julia_config(2)),
+    "julia1": dict(enc=encoder_config(hidden=384, heads=6, intermediate=1152, layers=22), julia=julia_config(2)),
     "julia1-384": dict(enc=encoder_config(hidden=384, heads=6, intermediate=576, layers=6), julia=julia_config(2)),
     "tiny": dict(enc=encoder_config(hidden=128, heads=2, intermediate=192, layers=3, local=16,
                                     vocab=512, max_positions=256), julia=julia_config(2)),

@@ -128,14 +128,17 @@ def test_gemm_rope(theta):
     assert np.all(d <= 4e-3 * scale + 1e-6), d.max()
 
 
-@pytest.mark.parametrize("splits", [0, 2, 5])
+@pytest.mark.parametrize("splits,k,rows", [(0, 1152, 70), (2, 1152, 70), (5, 1152, 70),
+                                           (0, 768, 70), (0, 384, 1), (0, 384, 33)])
 @pytest.mark.parametrize("epi", [abi.EPI_STORE_BF16, abi.EPI_ROPE_BF16, abi.EPI_GEGLU_BF16, abi.EPI_RESID_F32,
                                  abi.EPI_BIAS_BF16, abi.EPI_BIAS_RELU_BF16, abi.EPI_BIAS_F32])
-def test_gemm_splitk_matches_f64(epi, splits):
-    """Split-K (FP32 partials reduced in chunk order, then the epilogue) against the f64 product,
-    with the same per-epilogue tolerances as the single-pass GEMM; plus determinism."""
+def test_gemm_splitk_matches_f64(epi, splits, k, rows):
+    """Small-batch GEMMs against the f64 product, with the same per-epilogue tolerances as the single-pass
+    GEMM, plus determinism: split-K (FP32 partials reduced in chunk order, then the epilogue) for K = 1152
+    or a forced split count, and the one-launch small-batch kernel (K split over the four waves of a
+    workgroup, reduced in wave order) for K <= 768 with the split count left to the library."""
     r = rng(12)
-    rows, n, k = 70, 384, 1152
+    n = 384
     x, w, ref = _gemm_inputs(r, rows, n, k)
     bias = (r.standard_normal(n, dtype=np.float32) * 0.1).astype(np.float32)
     pos = r.integers(0, 8192, rows).astype(np.int32)
@@ -186,13 +189,15 @@ def test_gemm_splitk_matches_f64(epi, splits):
         assert np.all(d <= 4e-3 * sc + 2e-6), d.max()
 
 
-def test_gemm_splitk_gathered_rows():
+@pytest.mark.parametrize("splits", [4, 0])
+def test_gemm_splitk_gathered_rows(splits):
+    """Row-gathered X through the split-K pass (splits=4) and through the one-launch small-batch kernel."""
     r = rng(13)
     x, w, ref = _gemm_inputs(r, 300, 256, 512)
     idx = np.array([5, 0, 299, 17, 17, 100, 3], dtype=np.int32)
     out = torch.zeros(idx.size, 256, dtype=torch.float32, device="cuda")
     ws = torch.zeros(1 << 20, dtype=torch.uint8, device="cuda")
-    hip.op_gemm_splitk(abi.EPI_BIAS_F32, dev(x, BF16), dev(w, BF16), out, ws, splits=4, rows=idx.size,
+    hip.op_gemm_splitk(abi.EPI_BIAS_F32, dev(x, BF16), dev(w, BF16), out, ws, splits=splits, rows=idx.size,
                        gather=dev(idx), bias=dev(np.zeros(256, dtype=np.float32)))
     assert np.abs(host(out) - ref[idx]).max() < 1e-5
 
