@@ -159,11 +159,13 @@ void* jh_stream(jh_model* model);
 int jh_set_graph(jh_model* model, int enabled);
 
 /*
- * Split-K GEMMs (1 = on, default; 0 = off).  When a GEMM's output has too few
- * 128 x 128 tiles to occupy the GPU (small batches, marker rows), K is split
- * into chunks whose FP32 partial sums are reduced in a fixed order: results
- * are deterministic, but a row's FP32 summation order then depends on the
- * batch's token count.  Off, every output element is accumulated in the same
+ * Small-batch GEMM paths (1 = on, default; 0 = off).  When a GEMM's output has
+ * too few 128 x 128 tiles to occupy the GPU (small batches, marker rows), K is
+ * split: over the four waves of one workgroup (one launch, K <= 768) or into
+ * chunks whose FP32 partial sums a second kernel reduces (the residual GEMMs,
+ * with the residual add and LayerNorm in that kernel).  Either way the partial
+ * sums are added in a fixed order, so results are deterministic, but a row's
+ * FP32 summation order then depends on the batch's token count.  Off, every output element is accumulated in the same
  * order whatever the batch, so a row's logits are invariant to what else is
  * batched with it (to FP32 round-off of the bf16 activations, <= 1e-4), at
  * the cost of small-batch latency.  No reference counterpart (cuBLAS picks
