@@ -158,15 +158,23 @@ def test_invalid_batches_rejected(tiny):
     check_gates(s)
 
 
-def test_hidden_384_shape():
-    """The reference CUDA path's own hidden size (src/cuda/mod.rs:175) through the same kernels."""
-    cfg = synth.model_config("julia1-384")
+@pytest.mark.parametrize("shape", ["julia1-384", "julia1"])
+def test_hidden_384_shape(shape):
+    """The reference CUDA path's own hidden size (src/cuda/mod.rs:175) through the same kernels: a 6-layer cut
+    and the full 22-layer Julia-1 shape. The latter also runs a single ~160-token request, which takes the
+    small-batch GEMM paths."""
+    cfg = synth.model_config(shape)
     ws = abi.WeightSet(cfg, synth.make_weights(cfg, seed=5))
-    gpu, orc = hip.HipModel(ws), oracle.OracleModel(ws)
+    gpu, orc = hip.HipModel(ws), oracle.OracleModel(ws, threads=8)
     b = synth.make_batch([300, 64, 129, 7], [5, 3, 20, 2], cfg.vocab, 17)
     s = parity(b, gpu.forward(b), orc.forward(b))
-    print("h384", s)
+    print(shape, s)
     check_gates(s)
+    if shape == "julia1":
+        one = synth.make_batch([163], [4], cfg.vocab, 18)
+        s = parity(one, gpu.forward(one), orc.forward(one))
+        print(shape, "single request", s)
+        check_gates(s)
 
 
 def test_base_config4_slice(base):
