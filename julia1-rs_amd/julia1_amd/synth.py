@@ -36,7 +36,7 @@ def julia_config(head_layers=2):
     return {"format_version": 1, "weight_dtype": "float32", "head_layers": head_layers}
 
 
-# Named model shapes.  "modernbert-base" is the BASELINE shape.  "julia1" is
+# Named model shapes.  "modernbert-base" is the shape of BASELINE.json's configs.  "julia1" is
 # the reference's own model as its CUDA path and tests describe it: hidden 384
 # (src/cuda/mod.rs:175), Wqkv [1152, 384], Wi [2304, 384] and Wo [384, 1152]
 # (src/cpu/gemm.rs:380-438), 22 layers (README:212); the head-layer count is

@@ -1,7 +1,7 @@
 """Full encoder-forward parity on the GPU (jh_forward through the C-ABI)
 against the FP32 CPU oracle on identical synthetic weights and batches.
 
-Gates (BASELINE north_star): |Δlogit| <= 2e-2, |Δsoftmax| <= 1e-2 (f64
+Gates (BASELINE.json north_star): |Δlogit| <= 2e-2, |Δsoftmax| <= 1e-2 (f64
 softmax per row, as answers_from_logits, src/typed.rs:115-131), argmax
 agreement >= 99.9% (first-max rule, src/request.rs:164-172), token ids and
 positions bit-exact.
