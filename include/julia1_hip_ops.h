@@ -125,7 +125,9 @@ typedef struct jh_attn_tile {
  * K/Vᵀ staged in LDS, online softmax of scale·QKᵀ over keys with
  * |q_pos - k_pos| <= window (window < 0: all keys of the sequence).
  * q/k/v bf16 with row strides ldq/ldkv; head h reads columns [64h, 64h+64)
- * of each; out bf16 row stride ldo.  `tiles` is a device array.
+ * of each; out bf16 row stride ldo.  `tiles` is a device array; work items
+ * are dispatched in list order with heads varying fastest, so listing the
+ * costliest tiles first (as the backend does) balances the CUs.
  * Replaces attention_rope/attention_plain (src/cuda/kernels.cu:274-391); RoPE
  * is applied by the producing GEMM's ROPE epilogue instead of on every load.
  */

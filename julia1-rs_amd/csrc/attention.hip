@@ -55,8 +55,10 @@ __global__ __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(4))) void 
     __shared__ __align__(1024) bf16_t sK[2][KT * 64];
     __shared__ __align__(1024) bf16_t sV[2][KT * 64];
 
-    const AttnTile tile = a.tiles[blockIdx.x];
-    const int head = blockIdx.y;
+    // One workgroup per (tile, head), heads varying fastest: callers list the
+    // costliest tiles first, so those are dispatched first, one per CU.
+    const int head = (int)(blockIdx.x % (unsigned)a.heads);
+    const AttnTile tile = a.tiles[blockIdx.x / (unsigned)a.heads];
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lq = lane & 31, g = lane >> 5;
 
@@ -278,7 +280,7 @@ void launch_attention(const AttnArgs& a, hipStream_t s) {
     if (a.ldq % 8 || a.ldkv % 8 || a.ldo % 4 || a.ldq < a.heads * 64 || a.ldo < a.heads * 64 ||
         ((uintptr_t)a.q & 15) || ((uintptr_t)a.k & 15) || ((uintptr_t)a.v & 15) || ((uintptr_t)a.out & 7))
         throw jh_error(1, "attention: operands must be 16-byte aligned with row strides % 8 == 0");
-    if (a.ntiles > 0x7fffffff || a.heads > 65535) throw jh_error(1, "attention: grid too large");
-    JH_LAUNCH(attention_kernel, dim3(a.ntiles, a.heads), dim3(NTHR), 0, s, a);
+    if ((long)a.ntiles * a.heads > 0x7fffffffL) throw jh_error(1, "attention: grid too large");
+    JH_LAUNCH(attention_kernel, dim3((unsigned)(a.ntiles * a.heads)), dim3(NTHR), 0, s, a);
     HIP_CHECK(hipGetLastError());
 }

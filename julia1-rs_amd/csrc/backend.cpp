@@ -276,6 +276,13 @@ struct jh_model {
             for (uint32_t q0 = 0; q0 < lens[s]; q0 += QTILE)
                 tiles.push_back({(int32_t)(starts[s] + q0), (int32_t)std::min<uint32_t>(QTILE, lens[s] - q0),
                                  (int32_t)starts[s], (int32_t)lens[s], (int32_t)q0});
+        // Costliest first (queries x keys of a full-attention layer), so the
+        // attention kernel dispatches them first and every CU gets a mix of long
+        // and short work items; each tile writes only its own rows, so the
+        // order does not change results.
+        std::stable_sort(tiles.begin(), tiles.end(), [](const AttnTile& x, const AttnTile& y) {
+            return (int64_t)x.nq * x.kv_len > (int64_t)y.nq * y.kv_len;
+        });
         size_t mi = 0;
         for (size_t s = 0; s < nseq; ++s) {
             size_t first = mi;
