@@ -13,6 +13,8 @@
 // double-buffered: the DMA of K step kt+1 runs under the MFMAs of step kt,
 // one barrier per step, two resident workgroups per CU (64 KB LDS each); the
 // epilogue stages the tile through the same LDS for row-contiguous stores.
+// Outputs with more tiles than fit at once run persistent workgroups, which
+// also prefetch each next tile under the current one.
 //
 // Tiles are dealt XCD-contiguously: MI355X hands workgroups round-robin to its
 // 8 XCDs, so tile t goes to the workgroup whose id mod 8 selects the XCD that
@@ -21,6 +23,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 
 #include "../../include/julia1_hip_ops.h"
 #include "kernels.hpp"
@@ -325,6 +328,147 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     }
 }
 
+// Persistent variant of gemm_kernel for outputs with more tiles than resident
+// workgroups (two per CU): gridDim.x workgroups walk the tiles g, g + G, ...
+// (G a multiple of 8, so a workgroup stays in its XCD's band).  The DMA of the
+// next tile's first K step is issued at the current tile's last step into the
+// buffer that step does not read, so it lands under that step's MFMAs instead
+// of in front of the next tile.  Each wave waits for it before its epilogue,
+// whose stores (counted by vmcnt too) are then never waited on; the epilogue
+// stages through the last step's buffers, 8 KB per wave, in two 32-row passes.
+// Same products in the same K order as gemm_kernel, so results are identical.
+template <int EPI>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void gemm_persist_kernel(GemmArgs a) {
+    constexpr int BF = 128, BT = 128, FB = 2, TB = 2;
+    constexpr int CPR = BK / 8, RPI = 64 / CPR, IPW = BF / RPI / 4, STAGE = BF * BK;
+    __shared__ __align__(1024) bf16_t smem[4 * STAGE];
+    bf16_t* const sW = smem;
+    bf16_t* const sX = smem + 2 * STAGE;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nF = (a.n + BF - 1) / BF, nTk = (a.rows + BT - 1) / BT, ntiles = nF * nTk;
+    auto coords = [&](int b, int& f0, int& t0) {
+        const int xcd = b & 7, local = b >> 3, q8 = ntiles >> 3, r8 = ntiles & 7;
+        const int tile = xcd * q8 + (xcd < r8 ? xcd : r8) + local;
+        constexpr int GROUP = 8;
+        const int grp = tile / (GROUP * nF), gi = tile - grp * GROUP * nF;
+        const int gh = min(GROUP, nTk - grp * GROUP);
+        f0 = (gi / gh) * BF;
+        t0 = (grp * GROUP + gi % gh) * BT;
+    };
+    struct Src {
+        i32x4 rw, rx;
+        uint32_t woff[IPW], xoff[IPW];
+    };
+    auto setup = [&](int f0, int t0, Src& s) {
+        s.rw = make_rsrc(a.w + (long)f0 * a.k, (uint64_t)(a.n - f0) * a.k * 2);
+        s.rx = make_rsrc(a.x + (long)t0 * a.ldx, (uint64_t)(a.rows - 1 - t0) * a.ldx * 2 + (uint64_t)a.k * 2);
+#pragma unroll
+        for (int j = 0; j < IPW; ++j) {
+            const int lrow = (wave * IPW + j) * RPI + lane / CPR;
+            const int c = (lane % CPR) ^ swz(lrow);
+            s.woff[j] = (uint32_t)((min(f0 + lrow, a.n - 1) - f0) * a.k + c * 8) * 2;
+            const int t = min(t0 + lrow, a.rows - 1);
+            s.xoff[j] = (uint32_t)((t - t0) * (long)a.ldx + c * 8) * 2;
+        }
+    };
+    const uint32_t wl0 = (uint32_t)(uintptr_t)&sW[wave * IPW * 512];
+    const uint32_t xl0 = (uint32_t)(uintptr_t)&sX[wave * IPW * 512];
+    auto issue = [&](const Src& s, int kt, int st) {
+        const uint32_t kb = (uint32_t)kt * BK * 2;
+#pragma unroll
+        for (int j = 0; j < IPW; ++j) {
+            const uint32_t lw = __builtin_amdgcn_readfirstlane(wl0 + (st * STAGE + j * 512) * 2);
+            const uint32_t lx = __builtin_amdgcn_readfirstlane(xl0 + (st * STAGE + j * 512) * 2);
+            asm volatile("buffer_load_dwordx4 %1, %2, %3 offen lds" ::"{m0}"(lw), "v"(s.woff[j]), "s"(s.rw), "s"(kb)
+                         : "memory");
+            asm volatile("buffer_load_dwordx4 %1, %2, %3 offen lds" ::"{m0}"(lx), "v"(s.xoff[j]), "s"(s.rx), "s"(kb)
+                         : "memory");
+        }
+    };
+    const int wf = wave & 1, wt = wave >> 1, lr = lane & 31, lg = lane >> 5;
+    const int G = gridDim.x, KT = a.k / BK;
+    int cur = blockIdx.x, f0, t0, base = 0;
+    coords(cur, f0, t0);
+    Src sc;
+    setup(f0, t0, sc);
+    issue(sc, 0, 0);
+    bool first = true;
+    while (true) {
+        const int nxt = cur + G;
+        const bool has_next = nxt < ntiles;
+        int nf0 = 0, nt0 = 0;
+        Src sn = sc;
+        if (has_next) {
+            coords(nxt, nf0, nt0);
+            setup(nf0, nt0, sn);
+        }
+        f32x16 acc[FB][TB];
+#pragma unroll
+        for (int i = 0; i < FB; ++i)
+#pragma unroll
+            for (int j = 0; j < TB; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+        for (int kt = 0; kt < KT; ++kt) {
+            const int st = (base + kt) & 1;
+            // a later tile's step-0 DMA was waited for before the previous epilogue
+            if (kt > 0 || first) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+            if (kt + 1 < KT) issue(sc, kt + 1, st ^ 1);
+            else if (has_next) issue(sn, 0, st ^ 1);
+            const bf16_t* W = sW + st * STAGE;
+            const bf16_t* X = sX + st * STAGE;
+            bf16x8 af[2][FB], bx[2][TB];
+            auto load = [&](int ks, int s) {
+                const int c = ks * 2 + lg;
+#pragma unroll
+                for (int i = 0; i < FB; ++i) {
+                    const int r = wf * 64 + i * 32 + lr;
+                    af[s][i] = *(const bf16x8*)&W[r * BK + ((c ^ swz(r)) * 8)];
+                }
+#pragma unroll
+                for (int j = 0; j < TB; ++j) {
+                    const int r = wt * 64 + j * 32 + lr;
+                    bx[s][j] = *(const bf16x8*)&X[r * BK + ((c ^ swz(r)) * 8)];
+                }
+            };
+            load(0, 0);
+            load(1, 1);
+#pragma unroll
+            for (int ks = 0; ks < BK / 16; ++ks) {
+                const int s = ks & 1;
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int i = 0; i < FB; ++i)
+#pragma unroll
+                    for (int j = 0; j < TB; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[s][i], bx[s][j], acc[i][j], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+                if (ks + 2 < BK / 16) load(ks + 2, s);
+            }
+        }
+        const int st_last = (base + KT - 1) & 1;
+        __syncthreads();  // every wave is done reading the last step's buffers
+        if (has_next) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        float* stg = wave < 2 ? (float*)(sW + st_last * STAGE) + wave * 2048
+                              : (float*)(sX + st_last * STAGE) + (wave - 2) * 2048;
+        if (f0 + wf * 64 < a.n) {
+#pragma unroll
+            for (int j = 0; j < TB; ++j) {
+                f32x16 part[2][1] = {{acc[0][j]}, {acc[1][j]}};
+                epilogue<EPI, 1>(a, part, f0 + wf * 64, t0 + wt * 64 + j * 32, lane, stg);
+            }
+        }
+        if (!has_next) break;
+        cur = nxt;
+        f0 = nf0;
+        t0 = nt0;
+        sc = sn;
+        base = (base + KT) & 1;
+        first = false;
+    }
+}
+
 // Small batches in one launch, without the split-K workspace or its reduce
 // kernel.  A workgroup owns a 64-feature x 32-token tile and the whole K: every
 // operand chunk reaches LDS in a single round of DMA, laid out as K/64 blocks
@@ -550,6 +694,23 @@ bool use_small(const GemmArgs& a, long tiles) {
     return a.partial && a.splits == 0 && a.k <= SMALL_KMAX && splitk_count(a, tiles) > 1;
 }
 
+// Workgroups of gemm_kernel resident at once on the current device (two per
+// CU), rounded down to a multiple of 8 XCDs; the persistent kernel's grid.
+int resident_tiles() {
+    static std::atomic<int> cached[64];
+    int dev = 0;
+    HIP_CHECK(hipGetDevice(&dev));
+    if (dev < 0 || dev >= 64) throw jh_error(1, "gemm: device ordinal out of range");
+    int v = cached[dev].load(std::memory_order_relaxed);
+    if (v == 0) {
+        int cus = 0;
+        HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+        v = std::max(8, (2 * cus) / 8 * 8);
+        cached[dev].store(v, std::memory_order_relaxed);
+    }
+    return v;
+}
+
 template <int EPI>
 void launch_cfg(const GemmArgs& a, hipStream_t s) {
     constexpr int BF = 128, BT = 128;
@@ -574,7 +735,9 @@ void launch_cfg(const GemmArgs& a, hipStream_t s) {
         HIP_CHECK(hipGetLastError());
         return;
     }
+    const int resident = resident_tiles();
     if (a.gather) JH_LAUNCH((gemm_kernel<EPI, true>), dim3(blocks), dim3(256), 0, s, a);
+    else if (blocks > resident) JH_LAUNCH((gemm_persist_kernel<EPI>), dim3(resident), dim3(256), 0, s, a);
     else JH_LAUNCH((gemm_kernel<EPI, false>), dim3(blocks), dim3(256), 0, s, a);
     HIP_CHECK(hipGetLastError());
 }

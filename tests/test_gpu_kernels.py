@@ -32,7 +32,10 @@ def _gemm_inputs(r, rows, n, k):
     return x, w, x.astype(np.float64) @ w.astype(np.float64).T
 
 
-SHAPES = [(1, 64, 64), (37, 128, 768), (130, 384, 1152), (257, 2304, 768), (64, 768, 3072)]
+# The last two have more 128x128 tiles (520) than two per CU on MI355X, so they take the persistent
+# kernel (several tiles per workgroup, the next tile's first K step prefetched); K = 64 is its one-step case.
+SHAPES = [(1, 64, 64), (37, 128, 768), (130, 384, 1152), (257, 2304, 768), (64, 768, 3072),
+          (8300, 1024, 256), (8300, 1024, 64)]
 
 
 @pytest.mark.parametrize("rows,n,k", SHAPES)
@@ -59,10 +62,10 @@ def test_gemm_resid_f32(rows, n, k, with_bias):
     assert np.abs(host(out) - expect).max() < 1e-4 * math.sqrt(k) * 0.02 * 4 + 1e-5
 
 
+@pytest.mark.parametrize("rows,n,k", [(200, 384, 768), (8300, 1024, 128)])
 @pytest.mark.parametrize("epi", [abi.EPI_BIAS_BF16, abi.EPI_BIAS_RELU_BF16, abi.EPI_BIAS_F32])
-def test_gemm_bias_epilogues(epi):
+def test_gemm_bias_epilogues(epi, rows, n, k):
     r = rng(3)
-    rows, n, k = 200, 384, 768
     x, w, ref = _gemm_inputs(r, rows, n, k)
     bias = r.standard_normal(n, dtype=np.float32) * 0.1
     dt = torch.float32 if epi == abi.EPI_BIAS_F32 else BF16
@@ -85,7 +88,7 @@ def test_gemm_gather_rows():
     assert np.abs(host(out) - ref[idx]).max() < 1e-5
 
 
-@pytest.mark.parametrize("rows,inter,k", [(1, 64, 128), (77, 192, 128), (300, 1152, 768)])
+@pytest.mark.parametrize("rows,inter,k", [(1, 64, 128), (77, 192, 128), (300, 1152, 768), (8300, 512, 128)])
 def test_gemm_geglu(rows, inter, k):
     r = rng(5)
     x = bf16_round(r.standard_normal((rows, k), dtype=np.float32))
