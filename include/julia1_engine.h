@@ -8,8 +8,11 @@
  * src/weights.rs:32-94), resolve and shape-check every tensor
  * (`HostWeights::load`, src/model.rs:55-110), build the jh_model backend
  * (`assemble`, src/engine.rs:147-172), then run length-sorted micro-batches
- * (`batches`, src/engine.rs:191-210) through jh_forward with the nonfinite
- * check of `Engine::forward` (src/engine.rs:212-223).  Text encoding
+ * (`batches`, src/engine.rs:191-210) through the backend with the nonfinite
+ * check of `Engine::forward` (src/engine.rs:212-223).  Micro-batches are
+ * pipelined with jh_submit/jh_collect (up to JH_MAX_INFLIGHT ahead), so the
+ * host packs the next one while the GPU runs the current one; the logits
+ * equal those of one jh_forward per micro-batch.  Text encoding
  * (`Encoder`, src/encode.rs) is not part of this library: callers pass
  * token ids and marker positions, as `logits_encoded` receives them.
  *

@@ -133,7 +133,7 @@ int jh_forward_padded(jh_model* model, const uint32_t* ids, size_t batch, size_t
 /*
  * Split form of jh_forward, for callers that time or overlap the forward:
  *  jh_stage   validates the batch and enqueues its upload on the model's stream
- *             (waiting first for earlier work that may still read the pinned
+ *             (waiting first for its previous upload from the same pinned
  *             staging buffer);
  *  jh_execute enqueues the whole forward on the model's stream, reading the
  *             staged batch (repeatable; does not synchronise);
@@ -149,12 +149,39 @@ int jh_scores(jh_model* model, float* scores, size_t markers);
 void* jh_stream(jh_model* model);
 
 /*
- * Use a captured hipGraph for jh_execute (1 = on, 0 = off, default on): when
- * an execute has the same batch shape (tokens, markers, sequences, attention
- * tiles) as the previous one, its launch sequence is captured once and then
- * replayed while the shape stays unchanged; a shape seen for the first time
- * in a row runs eagerly, because capture and instantiation (~0.5 ms on
- * MI355X) cost more than replay saves.  No reference counterpart.
+ * Pipelined form of jh_forward, for engines that run several micro-batches in
+ * a row (`Engine::forward` over `batches`, src/engine.rs:191-223, which calls
+ * `CudaModel::forward` once per micro-batch and waits for each):
+ *  jh_submit  validates a batch, copies it into pinned staging, enqueues its
+ *             upload, the forward and the download of its scores on the
+ *             model's stream, and returns at once with a ticket (> 0);
+ *  jh_collect waits for that ticket's scores and copies its M scores out.
+ * While the GPU runs one batch the caller packs and submits the next, so the
+ * GPU does not idle between forwards on host work or on the round trip of a
+ * synchronous copy.  Forwards run in submission order on the one stream and
+ * give the same scores as jh_forward.  At most JH_MAX_INFLIGHT tickets may be
+ * outstanding (submitted, not yet collected); a further jh_submit fails with
+ * JH_ERR_INVALID.  Tickets may be collected in any order, each once; a failed
+ * jh_submit issues no ticket.  jh_collect waits without holding the model's
+ * lock, so another thread may submit meanwhile.  jh_submit also makes its batch
+ * the staged one (as jh_stage would) for jh_execute and the debug views.
+ * No reference counterpart.
+ */
+#define JH_MAX_INFLIGHT 2
+int jh_submit(jh_model* model, const uint32_t* ids, size_t tokens, const uint32_t* starts,
+              const uint32_t* lens, const uint8_t* qtypes, size_t sequences,
+              const uint32_t* marker_rows, size_t markers, uint64_t* ticket);
+int jh_collect(jh_model* model, uint64_t ticket, float* scores, size_t markers);
+
+/*
+ * Use a captured hipGraph for jh_execute, jh_forward and jh_submit (1 = on,
+ * 0 = off, default on): when a forward has the same batch shape (tokens,
+ * markers, sequences, attention tiles) as the previous one staged in the same
+ * staging buffer (one for jh_stage/jh_forward, one per jh_submit slot), its
+ * launch sequence is captured once and then replayed while the shape stays
+ * unchanged; a shape seen for the first time in a row runs eagerly, because
+ * capture and instantiation (~0.5 ms on MI355X) cost more than replay saves.
+ * No reference counterpart.
  */
 int jh_set_graph(jh_model* model, int enabled);
 

@@ -130,6 +130,31 @@ double gemm_bytes(int epi, double rows, double n, double k) {
     return rows * k * 2 + n * k * 2 + out;
 }
 
+// Device and pinned buffers of one staged batch's metadata (ids,
+// position|qtype words, attention tiles, marker rows), with the graph captured
+// for batches staged in it.  Slot 0 serves jh_stage/jh_forward; the others
+// form the jh_submit ring, where a slot stays busy until its ticket is
+// collected, so a batch's metadata and scores outlive the next batch's upload.
+struct MetaSlot {
+    DevBuf dev;
+    PinnedBuf host;
+    size_t cap = 0;                  // 32-bit words
+    hipEvent_t uploaded = nullptr;   // the upload from `host` has completed
+    bool upload_pending = false;
+    // jh_submit ring only
+    PinnedBuf scores;
+    size_t cap_scores = 0;           // floats
+    hipEvent_t done = nullptr;       // the scores have reached `scores`
+    bool busy = false, collecting = false;
+    uint64_t ticket = 0;
+    size_t markers = 0;
+    // graph of the launch sequence for the shape staged in this slot
+    hipGraphExec_t graph = nullptr;
+    size_t graph_key[6] = {0, 0, 0, 0, 0, 0};
+    // shape of the previous execute from this slot: captured only when it repeats
+    size_t last_key[6] = {0, 0, 0, 0, 0, 0};
+};
+
 }  // namespace
 
 struct jh_model {
@@ -146,10 +171,15 @@ struct jh_model {
     std::vector<HeadLayer> head;
     std::vector<std::pair<DevBuf, DevBuf>> ropes;
     // workspace (grow-only)
-    size_t cap_t = 0, cap_m = 0, cap_meta = 0;
+    size_t cap_t = 0, cap_m = 0;
     uint64_t ws_gen = 0;
-    DevBuf x, xn, qkv, ctx, hbuf, y, yn, qm, cm, hm, z, scores, meta;
-    PinnedBuf meta_host, scores_host;
+    DevBuf x, xn, qkv, ctx, hbuf, y, yn, qm, cm, hm, z, scores;
+    PinnedBuf scores_host;
+    // batch metadata: slot 0 for jh_stage/jh_forward, 1..kSlots-1 for jh_submit
+    static constexpr int kSlots = 1 + JH_MAX_INFLIGHT;
+    MetaSlot slots[kSlots];
+    int cur = 0;  // slot of the staged batch
+    uint64_t last_ticket = 0;
     // split-K partial sums of GEMMs whose output has too few tiles (small
     // batches, marker rows): fixed size, allocated with the model
     static constexpr size_t kSplitkBytes = 24u << 20;
@@ -162,14 +192,10 @@ struct jh_model {
     AttnTile* d_tiles = nullptr;
     AttnTile* d_mtiles = nullptr;
     int32_t* d_markers = nullptr;
-    // graph of the launch sequence for the staged shape
+    // replay repeated shapes from a captured graph (see jh_set_graph)
     bool use_graph = true;
     // split-K GEMMs for outputs with too few tiles (see jh_set_splitk)
     bool use_splitk = true;
-    hipGraphExec_t graph = nullptr;
-    size_t graph_key[6] = {0, 0, 0, 0, 0, 0};
-    // shape of the previous execute: a shape is captured only when it repeats
-    size_t last_key[6] = {0, 0, 0, 0, 0, 0};
     std::string name;
     // attention (query, key) pairs of the staged batch, for algorithmic FLOPs
     double pairs_global = 0, pairs_local = 0, pairs_marker = 0;
@@ -183,7 +209,11 @@ struct jh_model {
     std::function<void()> replay[K_COUNT];
 
     ~jh_model() {
-        if (graph) (void)hipGraphExecDestroy(graph);
+        for (MetaSlot& s : slots) {
+            if (s.graph) (void)hipGraphExecDestroy(s.graph);
+            if (s.uploaded) (void)hipEventDestroy(s.uploaded);
+            if (s.done) (void)hipEventDestroy(s.done);
+        }
         for (hipEvent_t e : ev_pool) (void)hipEventDestroy(e);
         if (stream) (void)hipStreamDestroy(stream);
     }
@@ -218,7 +248,12 @@ struct jh_model {
 
     void bind() const { HIP_CHECK(hipSetDevice(device)); }
 
-    void ensure_workspace(size_t t, size_t m, size_t meta_len) {
+    // Grows the workspace and the metadata buffers of `slot`.  Submitted
+    // forwards may still be running on the old buffers, so growth waits for
+    // the stream before it frees them.
+    void ensure_workspace(size_t t, size_t m, int slot, size_t meta_len) {
+        MetaSlot& ms = slots[slot];
+        if (t > cap_t || m > cap_m || meta_len > ms.cap) HIP_CHECK(hipStreamSynchronize(stream));
         if (t > cap_t || m > cap_m) {
             size_t ct = 1024, cm_ = 256;
             while (ct < std::max(t, cap_t)) ct <<= 1;
@@ -241,19 +276,22 @@ struct jh_model {
             cap_m = cm_;
             ++ws_gen;
         }
-        if (meta_len > cap_meta) {
+        if (meta_len > ms.cap) {
             size_t n = 4096;
             while (n < meta_len) n <<= 1;
-            meta.alloc(n * 4);
-            meta_host.alloc(n * 4);
-            cap_meta = n;
+            ms.dev.alloc(n * 4);
+            ms.host.alloc(n * 4);
+            ms.cap = n;
+            ms.upload_pending = false;
             ++ws_gen;
         }
+        if (!ms.uploaded) HIP_CHECK(hipEventCreateWithFlags(&ms.uploaded, hipEventDisableTiming));
     }
 
-    // Validates and uploads a packed batch (Batch, src/model.rs:114-124).
-    void stage(const uint32_t* ids, size_t t, const uint32_t* starts, const uint32_t* lens, const uint8_t* qtypes,
-               size_t nseq, const uint32_t* marker_rows, size_t m) {
+    // Validates a packed batch (Batch, src/model.rs:114-124) and enqueues its
+    // upload into metadata slot `slot`; the batch becomes the staged one.
+    void stage(int slot, const uint32_t* ids, size_t t, const uint32_t* starts, const uint32_t* lens,
+               const uint8_t* qtypes, size_t nseq, const uint32_t* marker_rows, size_t m) {
         // Recorded replays point into the staged batch's metadata and workspace.
         for (auto& r : replay) r = nullptr;
         if ((t && !ids) || (nseq && (!starts || !lens || !qtypes)) || (m && !marker_rows))
@@ -293,10 +331,13 @@ struct jh_model {
         }
         if (mi != m) throw jh_error(JH_ERR_INVALID, "marker rows must lie in their sequence, grouped by sequence");
         const size_t meta_len = 2 * t + 5 * (tiles.size() + mtiles.size()) + m;
-        ensure_workspace(t, m, meta_len);
-        // The previous upload may still be reading the pinned staging buffer.
-        HIP_CHECK(hipStreamSynchronize(stream));
-        uint32_t* hm_ = meta_host.as<uint32_t>();
+        ensure_workspace(t, m, slot, meta_len);
+        MetaSlot& ms = slots[slot];
+        // The slot's previous upload may still be reading its pinned staging buffer.
+        if (ms.upload_pending) HIP_CHECK(hipEventSynchronize(ms.uploaded));
+        ms.upload_pending = false;
+        staged = false;
+        uint32_t* hm_ = ms.host.as<uint32_t>();
         std::memcpy(hm_, ids, t * 4);
         uint32_t* tok = hm_ + t;
         for (size_t s = 0; s < nseq; ++s)
@@ -304,8 +345,11 @@ struct jh_model {
         std::memcpy(hm_ + 2 * t, tiles.data(), tiles.size() * sizeof(AttnTile));
         std::memcpy(hm_ + 2 * t + 5 * tiles.size(), mtiles.data(), mtiles.size() * sizeof(AttnTile));
         std::memcpy(hm_ + 2 * t + 5 * (tiles.size() + mtiles.size()), marker_rows, m * 4);
-        HIP_CHECK(hipMemcpyAsync(meta.p, meta_host.p, meta_len * 4, hipMemcpyHostToDevice, stream));
-        uint32_t* dm = meta.as<uint32_t>();
+        HIP_CHECK(hipMemcpyAsync(ms.dev.p, ms.host.p, meta_len * 4, hipMemcpyHostToDevice, stream));
+        HIP_CHECK(hipEventRecord(ms.uploaded, stream));
+        ms.upload_pending = true;
+        cur = slot;
+        uint32_t* dm = ms.dev.as<uint32_t>();
         d_ids = dm;
         d_tok = dm + t;
         d_tiles = (AttnTile*)(dm + 2 * t);
@@ -483,20 +527,23 @@ struct jh_model {
             run_all();
             return;
         }
+        MetaSlot& ms = slots[cur];
         const size_t key[6] = {T, M, S, ntiles, nmtiles, (size_t)ws_gen};
-        if (!graph || !std::equal(key, key + 6, graph_key)) {
+        if (!ms.graph || !std::equal(key, key + 6, ms.graph_key)) {
             // Capturing and instantiating the ~200-launch forward costs ~0.5 ms
             // on MI355X while replay saves nothing measurable over eager
             // launches, so a shape seen for the first time in a row runs
             // eagerly; the graph is built when the same shape comes again.
-            if (!std::equal(key, key + 6, last_key)) {
-                std::copy(key, key + 6, last_key);
+            if (!std::equal(key, key + 6, ms.last_key)) {
+                std::copy(key, key + 6, ms.last_key);
                 run_all();
                 return;
             }
-            if (graph) {
-                (void)hipGraphExecDestroy(graph);
-                graph = nullptr;
+            if (ms.graph) {
+                // a submitted forward may still be replaying it
+                HIP_CHECK(hipStreamSynchronize(stream));
+                (void)hipGraphExecDestroy(ms.graph);
+                ms.graph = nullptr;
             }
             HIP_CHECK(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
             try {
@@ -509,15 +556,15 @@ struct jh_model {
             }
             hipGraph_t g = nullptr;
             HIP_CHECK(hipStreamEndCapture(stream, &g));
-            hipError_t e = hipGraphInstantiate(&graph, g, nullptr, nullptr, 0);
+            hipError_t e = hipGraphInstantiate(&ms.graph, g, nullptr, nullptr, 0);
             (void)hipGraphDestroy(g);
             if (e != hipSuccess) {
-                graph = nullptr;
+                ms.graph = nullptr;
                 throw jh_error(JH_ERR_DEVICE, std::string("hipGraphInstantiate: ") + hipGetErrorString(e));
             }
-            std::copy(key, key + 6, graph_key);
+            std::copy(key, key + 6, ms.graph_key);
         }
-        HIP_CHECK(hipGraphLaunch(graph, stream));
+        HIP_CHECK(hipGraphLaunch(ms.graph, stream));
     }
 
     void read_scores(float* out, size_t m) {
@@ -530,6 +577,40 @@ struct jh_model {
         HIP_CHECK(hipMemcpyAsync(scores_host.p, scores.p, m * 4, hipMemcpyDeviceToHost, stream));
         HIP_CHECK(hipStreamSynchronize(stream));
         std::memcpy(out, scores_host.p, m * 4);
+    }
+
+    // jh_submit: stage into a free ring slot, enqueue the forward and the
+    // download of its scores, and return without waiting.
+    uint64_t submit(const uint32_t* ids, size_t t, const uint32_t* starts, const uint32_t* lens,
+                    const uint8_t* qtypes, size_t nseq, const uint32_t* marker_rows, size_t m) {
+        int slot = -1;
+        for (int i = 1; i < kSlots && slot < 0; ++i)
+            if (!slots[i].busy) slot = i;
+        if (slot < 0)
+            throw jh_error(JH_ERR_INVALID, "too many submitted batches in flight: collect one first");
+        MetaSlot& ms = slots[slot];
+        if (m > ms.cap_scores) {
+            size_t n = 256;
+            while (n < m) n <<= 1;
+            ms.scores.alloc(n * 4);
+            ms.cap_scores = n;
+        }
+        if (!ms.done) HIP_CHECK(hipEventCreateWithFlags(&ms.done, hipEventDisableTiming));
+        stage(slot, ids, t, starts, lens, qtypes, nseq, marker_rows, m);
+        execute();
+        if (m) HIP_CHECK(hipMemcpyAsync(ms.scores.p, scores.p, m * 4, hipMemcpyDeviceToHost, stream));
+        HIP_CHECK(hipEventRecord(ms.done, stream));
+        ms.busy = true;
+        ms.collecting = false;
+        ms.markers = m;
+        ms.ticket = ++last_ticket;
+        return ms.ticket;
+    }
+
+    MetaSlot& ticket_slot(uint64_t ticket) {
+        for (int i = 1; i < kSlots; ++i)
+            if (slots[i].busy && slots[i].ticket == ticket) return slots[i];
+        throw jh_error(JH_ERR_INVALID, "unknown or already collected ticket");
     }
 };
 
@@ -773,7 +854,7 @@ int jh_stage(jh_model* model, const uint32_t* ids, size_t tokens, const uint32_t
         if (!model) throw jh_error(JH_ERR_INVALID, "null model");
         std::lock_guard<std::mutex> g(model->mu);
         model->bind();
-        model->stage(ids, tokens, starts, lens, qtypes, sequences, marker_rows, markers);
+        model->stage(0, ids, tokens, starts, lens, qtypes, sequences, marker_rows, markers);
     });
 }
 
@@ -803,9 +884,46 @@ int jh_forward(jh_model* model, const uint32_t* ids, size_t tokens, const uint32
         if (markers && !scores) throw jh_error(JH_ERR_INVALID, "null scores buffer");
         std::lock_guard<std::mutex> g(model->mu);
         model->bind();
-        model->stage(ids, tokens, starts, lens, qtypes, sequences, marker_rows, markers);
+        model->stage(0, ids, tokens, starts, lens, qtypes, sequences, marker_rows, markers);
         model->execute();
         model->read_scores(scores, markers);
+    });
+}
+
+int jh_submit(jh_model* model, const uint32_t* ids, size_t tokens, const uint32_t* starts, const uint32_t* lens,
+              const uint8_t* qtypes, size_t sequences, const uint32_t* marker_rows, size_t markers,
+              uint64_t* ticket) {
+    return jh_guarded([&] {
+        if (!model || !ticket) throw jh_error(JH_ERR_INVALID, "null argument");
+        std::lock_guard<std::mutex> g(model->mu);
+        model->bind();
+        *ticket = model->submit(ids, tokens, starts, lens, qtypes, sequences, marker_rows, markers);
+    });
+}
+
+int jh_collect(jh_model* model, uint64_t ticket, float* scores, size_t markers) {
+    return jh_guarded([&] {
+        if (!model) throw jh_error(JH_ERR_INVALID, "null model");
+        hipEvent_t done;
+        {
+            std::lock_guard<std::mutex> g(model->mu);
+            MetaSlot& ms = model->ticket_slot(ticket);
+            if (ms.collecting) throw jh_error(JH_ERR_INVALID, "ticket is being collected by another call");
+            if (markers != ms.markers) throw jh_error(JH_ERR_INVALID, "score count does not match the submitted markers");
+            if (markers && !scores) throw jh_error(JH_ERR_INVALID, "null scores buffer");
+            ms.collecting = true;
+            done = ms.done;
+        }
+        // Wait without the model lock, so other threads can submit meanwhile;
+        // the slot stays busy, so its scores buffer and event stay put.
+        hipError_t e = hipSetDevice(model->device);
+        if (e == hipSuccess) e = hipEventSynchronize(done);
+        std::lock_guard<std::mutex> g(model->mu);
+        MetaSlot& ms = model->ticket_slot(ticket);
+        ms.collecting = false;
+        ms.busy = false;
+        if (e != hipSuccess) throw jh_error(JH_ERR_DEVICE, std::string("hipEventSynchronize: ") + hipGetErrorString(e));
+        if (markers) std::memcpy(scores, ms.scores.p, markers * 4);
     });
 }
 
@@ -835,7 +953,7 @@ int jh_forward_padded(jh_model* model, const uint32_t* ids, size_t batch, size_t
         if (m && (!markers || !scores)) throw jh_error(JH_ERR_INVALID, "null marker or score buffer");
         std::lock_guard<std::mutex> g(model->mu);
         model->bind();
-        model->stage(pids.data(), total, starts.data(), lens, qtypes, batch, rows.data(), rows.size());
+        model->stage(0, pids.data(), total, starts.data(), lens, qtypes, batch, rows.data(), rows.size());
         model->execute();
         model->read_scores(scores, m);
     });

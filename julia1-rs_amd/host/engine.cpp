@@ -10,6 +10,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <deque>
 #include <fstream>
 #include <memory>
 #include <mutex>
@@ -450,13 +451,46 @@ int je_logits_encoded(je_engine* e, size_t n, const uint32_t* ids, const size_t*
         }
         if (!group.empty()) batches.push_back(std::move(group));
         // Engine::forward per micro-batch: Batch::new packing (src/model.rs:127-147),
-        // the backend, then the nonfinite check (src/engine.rs:212-223).
+        // the backend, then the nonfinite check (src/engine.rs:212-223).  The
+        // reference waits for each forward before packing the next; here up to
+        // JH_MAX_INFLIGHT micro-batches are submitted ahead, so the host packs
+        // and enqueues batch i+1 while the GPU runs batch i.
+        struct InFlight {
+            uint64_t ticket;
+            size_t batch, markers;
+        };
+        std::deque<InFlight> inflight;
+        std::vector<float> scores;
+        // A failure leaves no ticket behind: outstanding ones are collected and dropped.
+        struct Drain {
+            je_engine* e;
+            std::deque<InFlight>& q;
+            ~Drain() {
+                std::vector<float> sink;
+                for (const InFlight& f : q) {
+                    sink.resize(f.markers);
+                    (void)jh_collect(e->model, f.ticket, sink.data(), f.markers);
+                }
+            }
+        } drain{e, inflight};
+        auto finish = [&] {
+            const InFlight f = inflight.front();
+            scores.assign(f.markers, 0.0f);
+            const int rc = jh_collect(e->model, f.ticket, scores.data(), f.markers);
+            inflight.pop_front();
+            if (rc != JH_OK) throw jh_error(rc, jh_last_error());
+            ++e->forwards;
+            for (float v : scores)
+                if (!std::isfinite(v)) throw jh_error(JH_ERR_NONFINITE, "Inference returned nonfinite logits");
+            size_t k = 0;
+            for (size_t i : batches[f.batch])
+                for (size_t j = mk_off[i]; j < mk_off[i + 1]; ++j) logits[j] = scores[k++];
+        };
         std::vector<uint32_t> bids, starts, lens, rows;
         std::vector<uint8_t> bq;
-        std::vector<float> scores;
-        for (const auto& items : batches) {
+        for (size_t bi = 0; bi < batches.size(); ++bi) {
             bids.clear(); starts.clear(); lens.clear(); rows.clear(); bq.clear();
-            for (size_t i : items) {
+            for (size_t i : batches[bi]) {
                 const uint32_t start = (uint32_t)bids.size();
                 starts.push_back(start);
                 lens.push_back((uint32_t)(id_off[i + 1] - id_off[i]));
@@ -464,17 +498,14 @@ int je_logits_encoded(je_engine* e, size_t n, const uint32_t* ids, const size_t*
                 bids.insert(bids.end(), ids + id_off[i], ids + id_off[i + 1]);
                 for (size_t j = mk_off[i]; j < mk_off[i + 1]; ++j) rows.push_back(start + markers[j]);
             }
-            scores.assign(rows.size(), 0.0f);
-            int rc = jh_forward(e->model, bids.data(), bids.size(), starts.data(), lens.data(), bq.data(), items.size(),
-                                rows.data(), rows.size(), scores.data());
+            if (inflight.size() == JH_MAX_INFLIGHT) finish();
+            uint64_t ticket = 0;
+            const int rc = jh_submit(e->model, bids.data(), bids.size(), starts.data(), lens.data(), bq.data(),
+                                     batches[bi].size(), rows.data(), rows.size(), &ticket);
             if (rc != JH_OK) throw jh_error(rc, jh_last_error());
-            ++e->forwards;
-            for (float v : scores)
-                if (!std::isfinite(v)) throw jh_error(JH_ERR_NONFINITE, "Inference returned nonfinite logits");
-            size_t k = 0;
-            for (size_t i : items)
-                for (size_t j = mk_off[i]; j < mk_off[i + 1]; ++j) logits[j] = scores[k++];
+            inflight.push_back({ticket, bi, rows.size()});
         }
+        while (!inflight.empty()) finish();
     });
 }
 

@@ -16,7 +16,8 @@ from . import abi
 _lib = None
 
 EXPORTS = (
-    "jh_create", "jh_forward", "jh_forward_padded", "jh_stage", "jh_execute", "jh_scores", "jh_stream",
+    "jh_create", "jh_forward", "jh_forward_padded", "jh_stage", "jh_execute", "jh_scores", "jh_stream", "jh_submit",
+    "jh_collect",
     "jh_set_graph", "jh_set_splitk", "jh_name", "jh_destroy", "jh_last_error", "jh_rope_table", "jh_debug_tokens",
     "jh_debug_encode", "jh_profile", "jh_profile_read", "jh_profile_replay",
     "jh_op_gemm", "jh_op_gemm_splitk", "jh_op_interleave_geglu", "jh_op_embed_ln", "jh_op_layer_norm", "jh_op_final_norm",
@@ -48,6 +49,8 @@ def lib():
         L.jh_stage.argtypes = [vp, vp, sz, vp, vp, vp, sz, vp, sz]
         L.jh_execute.argtypes = [vp]
         L.jh_scores.argtypes = [vp, vp, sz]
+        L.jh_submit.argtypes = [vp, vp, sz, vp, vp, vp, sz, vp, sz, C.POINTER(C.c_uint64)]
+        L.jh_collect.argtypes = [vp, C.c_uint64, vp, sz]
         L.jh_stream.argtypes = [vp]
         L.jh_stream.restype = vp
         L.jh_set_graph.argtypes = [vp, C.c_int]
@@ -128,6 +131,19 @@ class HipModel:
         check(lib().jh_forward_padded(self.h, _p(ids), B, L, _p(lens), _p(qtypes), _p(markers), _p(marker_starts),
                                       _p(scores)))
         return scores
+
+    def submit(self, b) -> int:
+        """jh_submit: enqueue a forward without waiting; returns its ticket."""
+        t = C.c_uint64(0)
+        check(lib().jh_submit(self.h, _p(b.ids), b.tokens, _p(b.starts), _p(b.lens), _p(b.qtypes), b.lens.size,
+                              _p(b.marker_rows), b.marker_rows.size, C.byref(t)))
+        return t.value
+
+    def collect(self, ticket: int, m: int) -> np.ndarray:
+        """jh_collect: wait for a submitted forward and return its m scores."""
+        out = np.zeros(m, dtype=np.float32)
+        check(lib().jh_collect(self.h, ticket, _p(out), m))
+        return out
 
     def stage(self, b):
         self._staged = b

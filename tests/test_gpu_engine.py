@@ -75,3 +75,23 @@ def test_bf16_checkpoint_gives_identical_logits(setup, tmp_path):
     for w, g, r, o in zip(want, got, rough, ref):
         assert np.array_equal(w.view(np.uint32), g.view(np.uint32))
         assert np.abs(r - o).max() <= 2e-2
+
+
+def test_nonfinite_logits_drain_pipelined_batches(setup, tmp_path):
+    """Engine::forward's nonfinite check (src/engine.rs:212-223) with micro-batches submitted
+    ahead: the error surfaces, the batches still in flight are collected and dropped, and the
+    engine keeps working (a second call fails the same way rather than on leaked tickets)."""
+    from julia1_amd import hip
+    root, cfg, _ = setup
+    t = synth.make_weights(cfg, seed=21)
+    t["scorer.3.weight"] = np.full_like(t["scorer.3.weight"], np.nan)
+    bad = str(tmp_path / "nan")
+    synth.write_checkpoint(bad, "tiny", t)
+    e = engine.Engine.load(bad, batch_size=2)
+    b = synth.make_batch([50, 3, 200, 17, 90, 64, 1, 130], [2, 1, 6, 3, 4, 5, 1, 20], cfg.vocab, 15)
+    items = list(b.items())
+    for _ in range(2):
+        with pytest.raises(hip.HipError, match="nonfinite"):
+            e.logits_encoded(items)
+    good = engine.Engine.load(root, batch_size=2)
+    assert len(good.logits_encoded(items)) == len(items)

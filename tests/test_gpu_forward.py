@@ -140,6 +140,67 @@ def test_graph_replay_matches_eager(base):
     gpu.set_graph(True)
 
 
+def test_submit_collect_matches_forward(base):
+    """jh_submit/jh_collect (pipelined forwards) give jh_forward's scores bit for bit, in any
+    collection order; the in-flight limit, double collection and a wrong marker count are errors
+    that leave the outstanding tickets collectable."""
+    ws, gpu, _ = base
+    w = synth.workload("config1")
+    b1, b2, b3 = w.subset(range(6)), w.subset(range(6, 13)), w.subset([20])
+    r1, r2, r3 = gpu.forward(b1), gpu.forward(b2), gpu.forward(b3)
+    for _ in range(2):  # the second round replays the shapes from captured graphs
+        t1, t2 = gpu.submit(b1), gpu.submit(b2)
+        assert t2 > t1 > 0
+        with pytest.raises(hip.HipError, match="in flight"):
+            gpu.submit(b3)
+        with pytest.raises(hip.HipError, match="score count"):
+            gpu.collect(t2, b2.marker_rows.size + 1)
+        assert np.array_equal(gpu.collect(t2, b2.marker_rows.size), r2)
+        with pytest.raises(hip.HipError, match="already collected"):
+            gpu.collect(t2, b2.marker_rows.size)
+        t3 = gpu.submit(b3)
+        assert np.array_equal(gpu.collect(t1, b1.marker_rows.size), r1)
+        assert np.array_equal(gpu.collect(t3, b3.marker_rows.size), r3)
+    # the synchronous path still sees its own batch after submits
+    assert np.array_equal(gpu.forward(b2), r2)
+
+
+def test_submit_grows_workspace_while_in_flight(tiny):
+    """A submitted batch larger than the workspace reallocates it while an earlier forward is in
+    flight: the growth waits for that forward, and both results match the oracle."""
+    ws, _, orc = tiny
+    gpu = hip.HipModel(ws)  # fresh: the workspace starts at its minimum size
+    small = synth.make_batch([20, 7], [2, 1], ws.cfg.vocab, 31)
+    big = synth.make_batch([200] * 16, [4] * 16, ws.cfg.vocab, 32)
+    ts = gpu.submit(small)
+    tb = gpu.submit(big)
+    got_b = gpu.collect(tb, big.marker_rows.size)
+    got_s = gpu.collect(ts, small.marker_rows.size)
+    check_gates(parity(small, got_s, orc.forward(small)))
+    check_gates(parity(big, got_b, orc.forward(big)))
+    assert np.array_equal(got_s, gpu.forward(small))
+    assert np.array_equal(got_b, gpu.forward(big))
+    gpu.close()
+
+
+def test_collect_waits_without_blocking_submit(tiny):
+    """jh_collect waits without the model lock: another thread submits and collects meanwhile."""
+    import threading
+    ws, gpu, _ = tiny
+    b1 = synth.make_batch([120, 64, 200], [3, 2, 5], ws.cfg.vocab, 33)
+    b2 = synth.make_batch([30, 9], [2, 2], ws.cfg.vocab, 34)
+    r1, r2 = gpu.forward(b1), gpu.forward(b2)
+    t1 = gpu.submit(b1)
+    out = {}
+    th = threading.Thread(target=lambda: out.update(a=gpu.collect(t1, b1.marker_rows.size)))
+    th.start()
+    t2 = gpu.submit(b2)
+    got2 = gpu.collect(t2, b2.marker_rows.size)
+    th.join(timeout=60)
+    assert not th.is_alive()
+    assert np.array_equal(out["a"], r1) and np.array_equal(got2, r2)
+
+
 def test_invalid_batches_rejected(tiny):
     ws, gpu, _ = tiny
     b = synth.make_batch([10, 5], [2, 1], ws.cfg.vocab, 1)
