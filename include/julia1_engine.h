@@ -77,6 +77,10 @@ int je_logits_encoded(je_engine* engine, size_t items, const uint32_t* ids, cons
 /* The parsed configuration; pointers inside stay valid while the engine lives. */
 int je_config(je_engine* engine, jh_config* out);
 
+/* The engine's options after je_load resolved them (`Engine::options`,
+ * src/engine.rs:174-176): max_length is the effective limit. */
+int je_get_options(je_engine* engine, je_options* out);
+
 /* `Engine::device_name` (src/engine.rs:277-283): "hip:N (<device name>)". */
 const char* je_device_name(je_engine* engine);
 

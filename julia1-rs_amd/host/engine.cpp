@@ -516,6 +516,13 @@ int je_config(je_engine* e, jh_config* out) {
     });
 }
 
+int je_get_options(je_engine* e, je_options* out) {
+    return jh_guarded([&] {
+        if (!e || !out) invalid("null argument");
+        *out = e->options;
+    });
+}
+
 const char* je_device_name(je_engine* e) { return e ? e->name.c_str() : ""; }
 
 uint64_t je_forward_count(je_engine* e) { return e ? e->forwards : 0; }

@@ -1,6 +1,9 @@
-// Minimal JSON reader for checkpoint configs and safetensors headers:
-// objects (insertion-ordered), arrays, strings (with \uXXXX escapes),
-// numbers (kept as double plus an "is integer" flag), true/false/null.
+// JSON reader (RFC 8259 grammar) for checkpoint configs, safetensors headers
+// and request documents: objects keep insertion order (a repeated key keeps
+// its first position and takes the last value, as Python dicts and
+// serde_json's preserve_order maps do), arrays, strings (\uXXXX escapes with
+// surrogate pairs), numbers (the literal text, its double value and an "is
+// integer" flag), true/false/null.  Nesting is limited to 128 levels.
 #pragma once
 
 #include <cstdint>
@@ -19,6 +22,7 @@ struct Json {
     bool b = false;
     double num = 0.0;
     bool integral = false;  // number written without fraction/exponent
+    std::string raw;        // number: the literal text
     std::string str;
     std::vector<Json> arr;
     std::vector<std::pair<std::string, Json>> obj;
@@ -58,11 +62,35 @@ private:
         }
         return false;
     }
+    int depth_ = 0;
+    struct Nest {
+        int& d;
+        explicit Nest(JsonParser& p) : d(p.depth_) {
+            if (++d > 128) throw std::runtime_error("invalid JSON: recursion limit exceeded");
+        }
+        ~Nest() { --d; }
+    };
     Json value() {
         ws();
         if (p_ >= end_) fail("unexpected end");
         Json v;
         char c = *p_;
+        if (c == '{' || c == '[') {
+            Nest n(*this);
+            return container(c);
+        }
+        if (c == '"') {
+            v.kind = Json::String;
+            v.str = string();
+            return v;
+        }
+        if (lit("true")) { v.kind = Json::Bool; v.b = true; return v; }
+        if (lit("false")) { v.kind = Json::Bool; v.b = false; return v; }
+        if (lit("null")) return v;
+        return number();
+    }
+    Json container(char c) {
+        Json v;
         if (c == '{') {
             ++p_;
             v.kind = Json::Object;
@@ -75,7 +103,11 @@ private:
                 ws();
                 if (p_ >= end_ || *p_ != ':') fail("expected ':'");
                 ++p_;
-                v.obj.emplace_back(std::move(k), value());
+                Json item = value();
+                bool seen = false;
+                for (auto& kv : v.obj)
+                    if (kv.first == k) { kv.second = std::move(item); seen = true; break; }
+                if (!seen) v.obj.emplace_back(std::move(k), std::move(item));
                 ws();
                 if (p_ < end_ && *p_ == ',') { ++p_; continue; }
                 if (p_ < end_ && *p_ == '}') { ++p_; return v; }
@@ -95,34 +127,38 @@ private:
                 fail("expected ',' or ']'");
             }
         }
-        if (c == '"') {
-            v.kind = Json::String;
-            v.str = string();
-            return v;
-        }
-        if (lit("true")) { v.kind = Json::Bool; v.b = true; return v; }
-        if (lit("false")) { v.kind = Json::Bool; v.b = false; return v; }
-        if (lit("null")) return v;
-        return number();
+        fail("bad value");
     }
+    bool digit() const { return p_ < end_ && *p_ >= '0' && *p_ <= '9'; }
+    // -? (0 | [1-9][0-9]*) (. [0-9]+)? ([eE] [+-]? [0-9]+)?
     Json number() {
         const char* s = p_;
         bool integral = true;
-        if (p_ < end_ && (*p_ == '-' || *p_ == '+')) ++p_;
-        bool digits = false;
-        while (p_ < end_) {
-            char c = *p_;
-            if (c >= '0' && c <= '9') { digits = true; ++p_; continue; }
-            if (c == '.' || c == 'e' || c == 'E' || c == '+' || c == '-') { integral = false; ++p_; continue; }
-            break;
+        if (p_ < end_ && *p_ == '-') ++p_;
+        if (!digit()) fail("bad value");
+        if (*p_ == '0') {
+            ++p_;
+            if (digit()) fail("leading zero");
+        } else {
+            while (digit()) ++p_;
         }
-        if (!digits) fail("bad value");
-        std::string t(s, p_);
-        char* e = nullptr;
+        if (p_ < end_ && *p_ == '.') {
+            integral = false;
+            ++p_;
+            if (!digit()) fail("bad number");
+            while (digit()) ++p_;
+        }
+        if (p_ < end_ && (*p_ == 'e' || *p_ == 'E')) {
+            integral = false;
+            ++p_;
+            if (p_ < end_ && (*p_ == '+' || *p_ == '-')) ++p_;
+            if (!digit()) fail("bad number");
+            while (digit()) ++p_;
+        }
         Json v;
         v.kind = Json::Number;
-        v.num = std::strtod(t.c_str(), &e);
-        if (!e || *e) fail("bad number");
+        v.raw.assign(s, p_);
+        v.num = std::strtod(v.raw.c_str(), nullptr);  // out of range -> +-inf or 0, like a parsed Python float
         v.integral = integral;
         return v;
     }
@@ -154,6 +190,7 @@ private:
         std::string o;
         while (p_ < end_ && *p_ != '"') {
             char c = *p_++;
+            if ((unsigned char)c < 0x20) fail("control character in string");
             if (c != '\\') { o += c; continue; }
             if (p_ >= end_) fail("bad escape");
             char e = *p_++;
@@ -168,9 +205,12 @@ private:
                 case 't': o += '\t'; break;
                 case 'u': {
                     uint32_t cp = hex4();
-                    if (cp >= 0xD800 && cp < 0xDC00 && end_ - p_ >= 6 && p_[0] == '\\' && p_[1] == 'u') {
+                    if (cp >= 0xDC00 && cp < 0xE000) fail("lone trailing surrogate");
+                    if (cp >= 0xD800 && cp < 0xDC00) {
+                        if (end_ - p_ < 6 || p_[0] != '\\' || p_[1] != 'u') fail("lone leading surrogate");
                         p_ += 2;
                         uint32_t lo = hex4();
+                        if (lo < 0xDC00 || lo >= 0xE000) fail("lone leading surrogate");
                         cp = 0x10000 + ((cp - 0xD800) << 10) + (lo - 0xDC00);
                     }
                     put_utf8(o, cp);

@@ -28,6 +28,7 @@ def _lib():
         L.je_load.argtypes = [C.c_char_p, vp, C.POINTER(vp)]
         L.je_logits_encoded.argtypes = [vp, sz, vp, vp, vp, vp, vp, vp]
         L.je_config.argtypes = [vp, vp]
+        L.je_get_options.argtypes = [vp, vp]
         L.je_device_name.argtypes = [vp]
         L.je_device_name.restype = C.c_char_p
         L.je_forward_count.argtypes = [vp]

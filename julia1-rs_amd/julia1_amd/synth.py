@@ -121,6 +121,50 @@ def write_checkpoint(root: str, shape: str, tensors: dict) -> str:
     return root
 
 
+# Special tokens of the synthetic tokenizer, in id order; tokenizer_config.json
+# names them as a Julia-1 checkpoint's does (src/encode.rs:70-83).
+SPECIAL_TOKENS = ("[PAD]", "[UNK]", "[CLS]", "[SEP]", "<mask>")
+TOKENIZER_CONFIG = {"mask_token": "<mask>", "cls_token": "[CLS]", "sep_token": "[SEP]", "pad_token": "[PAD]",
+                    "unk_token": "[UNK]"}
+_WORDS = ("x", "the", "a", "to", "of", "and", "in", "is", "it", "you", "that", "for", "on", "with", "as", "player",
+          "game", "turn", "card", "move", "score", "team", "route", "billing", "access", "login", "payments", "low",
+          "medium", "high", "rate", "choose", "question", "choice", "noul", "true", "false", "option", "state",
+          "context", "plain", "text", "word", "number", "largest", "approve", "review", "human", "run", "value")
+
+
+def train_tokenizer(vocab_size: int = 500):
+    """A byte-level BPE `tokenizers.Tokenizer` trained on a seeded synthetic corpus: the stand-in for a
+    checkpoint's tokenizer.json (absent here).  " x" is a single token, as in the Julia-1 tokenizer
+    (tests/checkpoint.rs:45-46)."""
+    from tokenizers import Tokenizer, decoders, models, pre_tokenizers, trainers
+    rng = np.random.default_rng(1234)
+    corpus = []
+    for _ in range(3000):
+        n = int(rng.integers(3, 14))
+        words = [_WORDS[int(i)] for i in rng.integers(0, len(_WORDS), n)]
+        corpus.append(" ".join(words) + ("." if rng.random() < 0.5 else ""))
+        corpus.append(" ".join(["x"] * int(rng.integers(1, 6))))
+        corpus.append(json.dumps({"score": int(rng.integers(0, 100)), "team": _WORDS[int(rng.integers(0, 50))]}))
+    tok = Tokenizer(models.BPE())
+    tok.pre_tokenizer = pre_tokenizers.ByteLevel(add_prefix_space=False)
+    tok.decoder = decoders.ByteLevel()
+    trainer = trainers.BpeTrainer(vocab_size=vocab_size, special_tokens=list(SPECIAL_TOKENS), show_progress=False,
+                                  initial_alphabet=pre_tokenizers.ByteLevel.alphabet())
+    tok.train_from_iterator(corpus, trainer)
+    return tok
+
+
+def write_tokenizer(root: str, vocab_size: int = 500) -> str:
+    """<root>/tokenizer/{tokenizer.json, tokenizer_config.json}, where `Engine::load` reads the encoder
+    (src/engine.rs:100-107)."""
+    d = os.path.join(root, "tokenizer")
+    os.makedirs(d, exist_ok=True)
+    train_tokenizer(vocab_size).save(os.path.join(d, "tokenizer.json"))
+    with open(os.path.join(d, "tokenizer_config.json"), "w") as f:
+        json.dump(TOKENIZER_CONFIG, f)
+    return d
+
+
 class SplitMix64:
     """SplitMix64 stream (Steele, Lea, Flood 2014), vectorised over numpy uint64."""
     GAMMA = np.uint64(0x9E3779B97F4A7C15)

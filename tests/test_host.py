@@ -18,7 +18,7 @@ def declared_functions():
         if f.endswith(".h"):
             text = open(os.path.join(ROOT, "include", f)).read()
             text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-            names += re.findall(r"^\s*(?:const\s+)?[\w]+\s*\**\s*(j[he]_\w+)\s*\(", text, flags=re.M)
+            names += re.findall(r"^\s*(?:const\s+)?[\w]+\s*\**\s*(j[het]_\w+)\s*\(", text, flags=re.M)
     return sorted(set(names))
 
 
@@ -29,6 +29,8 @@ def test_library_exports_every_declared_symbol():
     missing = [n for n in names if not hasattr(lib, n)]
     assert not missing, missing
     assert set(hip.EXPORTS) <= set(names)
+    from julia1_amd import text
+    assert set(text.EXPORTS) <= set(names)
 
 
 def test_last_error_is_empty_string_initially():
