@@ -932,6 +932,8 @@ int jh_forward_padded(jh_model* model, const uint32_t* ids, size_t batch, size_t
     return jh_guarded([&] {
         if (!model) throw jh_error(JH_ERR_INVALID, "null model");
         if (batch && (!ids || !lens || !qtypes || !marker_starts)) throw jh_error(JH_ERR_INVALID, "null batch array");
+        const size_t m = batch ? marker_starts[batch] : 0;
+        if (m && (!markers || !scores)) throw jh_error(JH_ERR_INVALID, "null marker or score buffer");
         // Pack away the padding on the host: the device only ever sees real tokens.
         std::vector<uint32_t> pids, starts(batch), rows;
         size_t total = 0;
@@ -943,14 +945,13 @@ int jh_forward_padded(jh_model* model, const uint32_t* ids, size_t batch, size_t
         pids.reserve(total);
         for (size_t b = 0; b < batch; ++b) {
             pids.insert(pids.end(), ids + b * padded_len, ids + b * padded_len + lens[b]);
-            if (marker_starts[b + 1] < marker_starts[b]) throw jh_error(JH_ERR_INVALID, "marker_starts must be non-decreasing");
+            if (marker_starts[b + 1] < marker_starts[b] || marker_starts[b + 1] > m)
+                throw jh_error(JH_ERR_INVALID, "marker_starts must be non-decreasing");
             for (uint32_t j = marker_starts[b]; j < marker_starts[b + 1]; ++j) {
                 if (markers[j] >= lens[b]) throw jh_error(JH_ERR_INVALID, "marker outside its row");
                 rows.push_back(starts[b] + markers[j]);
             }
         }
-        const size_t m = batch ? marker_starts[batch] : 0;
-        if (m && (!markers || !scores)) throw jh_error(JH_ERR_INVALID, "null marker or score buffer");
         std::lock_guard<std::mutex> g(model->mu);
         model->bind();
         model->stage(0, pids.data(), total, starts.data(), lens, qtypes, batch, rows.data(), rows.size());

@@ -214,6 +214,17 @@ def test_invalid_batches_rejected(tiny):
     long = synth.make_batch([ws.cfg.max_positions + 1], [1], ws.cfg.vocab, 1)
     with pytest.raises(hip.HipError):
         gpu.forward(long)
+    # padded entry point: a null marker array and marker_starts past the marker count are errors, not reads
+    ids = np.zeros((2, 10), dtype=np.uint32)
+    lens = np.array([10, 5], dtype=np.uint32)
+    qt = np.zeros(2, dtype=np.uint8)
+    mst = np.array([0, 2, 3], dtype=np.uint32)
+    scores = np.zeros(3, dtype=np.float32)
+    rc = hip.lib().jh_forward_padded(gpu.h, hip._p(ids), 2, 10, hip._p(lens), hip._p(qt), None, hip._p(mst),
+                                     hip._p(scores))
+    assert rc == 1 and "null marker" in hip.lib().jh_last_error().decode()
+    with pytest.raises(hip.HipError, match="marker_starts"):
+        gpu.forward_padded(ids, lens, qt, np.zeros(3, np.uint32), np.array([0, 4, 3], dtype=np.uint32))
     # the model still works after rejected calls
     s = parity(b, gpu.forward(b), tiny[2].forward(b))
     check_gates(s)
