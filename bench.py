@@ -36,6 +36,18 @@ ENCODER_GEMMS = ("gemm_qkv_rope", "gemm_wo_resid", "gemm_wi_geglu", "gemm_wo2_re
 MFMA_CLASSES = ENCODER_GEMMS + ("attn_global", "attn_local", "head_gemm", "head_attn")
 
 
+def cpu_model_name():
+    """The host CPU's model string (first 'model name' line of /proc/cpuinfo), or None."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
@@ -357,6 +369,18 @@ def main():
                 t4.append(time.perf_counter() - tc)
             cpu["value_4_threads"] = round(tokens / statistics.median(t4), 1)
             log(f"cpu oracle: {statistics.median(t4):.2f} s/forward on 4 threads")
+        # configs[0] (one 128-token request) on the same oracle and threads, and the host it ran on.
+        b0 = synth.workload("config0")
+        orc.forward(b0)
+        t0 = []
+        for _ in range(5):
+            tc = time.perf_counter()
+            orc.forward(b0)
+            t0.append(time.perf_counter() - tc)
+        cpu["config0_ms"] = round(statistics.median(t0) * 1e3, 2)
+        cpu["host"] = dict(cpu_model=cpu_model_name(), cpus_visible=len(os.sched_getaffinity(0)),
+                           cpus_total=os.cpu_count())
+        log(f"cpu oracle: config0 {cpu['config0_ms']} ms/forward on {threads} threads; host {cpu['host']}")
 
     out = {
         "metric": METRIC, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
