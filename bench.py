@@ -112,15 +112,26 @@ def reference_protocol(np, synth, engine):
 
     Rows are synthetic: single requests ~U[140,180] tokens (the published ~160), the 2000-row batch
     ~U[32,554] (the published mean of ~293 tokens per row), 2-8 options per row, long requests of 933, 3928
-    and 7556 tokens with 4 options. Tokenization is not part of these timings (there is no tokenizer here);
-    it is part of the reference's."""
+    and 7556 tokens with 4 options, given as token ids. Tokenization is part of the reference's figures; the
+    "text" leg (text_protocol) repeats the single and batch legs from text rows when `tokenizers` is present."""
     import shutil
     import tempfile
+    try:
+        import tokenizers  # noqa: F401  (the text leg needs the tokenizers library)
+        from julia1_amd import text
+    except ImportError:
+        text = None
     cfg = synth.model_config("julia1")
     root = tempfile.mkdtemp(prefix="julia1_ckpt_")
+    te = None
     try:
         synth.write_checkpoint(root, "julia1", synth.make_weights(cfg, seed=0))
-        e = engine.Engine.load(root, "hip:0", batch_size=16, max_batch_tokens=65536)
+        if text is not None:
+            synth.write_tokenizer(root)
+            te = text.TextEngine.load(root, "hip:0", batch_size=16, max_batch_tokens=65536)
+            e = te.engine
+        else:
+            e = engine.Engine.load(root, "hip:0", batch_size=16, max_batch_tokens=65536)
     finally:
         shutil.rmtree(root, ignore_errors=True)
     rng = np.random.default_rng(7)
@@ -146,15 +157,62 @@ def reference_protocol(np, synth, engine):
     best = min(_timed(lambda: e.logits_encoded(batch)) for _ in range(3))
     long_ms = {str(n): round(min(_timed(lambda: e.logits_encoded(it)) for _ in range(3)) * 1e3, 3)
                for n, it in longs.items()}
+    text_leg = text_protocol(np, synth, te) if te is not None else None
     out = dict(shape="julia1: hidden 384, 6x64 heads, GEGLU 1152, 22 layers, 2 head layers (synthetic weights)",
                single=dict(n=len(lat), mean_ms=round(float(np.mean(lat)), 3), p50_ms=round(lat[len(lat) // 2], 3),
                            p99_ms=round(lat[int(0.99 * (len(lat) - 1))], 3)),
                batch=dict(n=len(batch), tokens=int(sum(len(i[0]) for i in batch)), best_s=round(best, 4),
                           rows_per_s=round(len(batch) / best, 1)),
                long_best_ms=long_ms, reference_cuda=REFERENCE_CUDA,
-               note="tokenization excluded here, included in the reference's figures")
+               note="token ids in: tokenization excluded here, included in the reference's figures")
+    if text_leg is not None:
+        out["text"] = text_leg
     e.close()
     return out
+
+
+def text_protocol(np, synth, te):
+    """The single-request and batch legs again, from text rows through the text front end (request
+    parsing, Encoder::sequence with its caches, tokenization, engine, logits), as the reference's figures are.
+    The tokenizer is the synthetic byte-level BPE stand-in (`tokenizers` library, called back from the C++
+    encoder through Python), as the real checkpoint's tokenizer.json is absent; rows are random words of its
+    corpus, sized to ~160 tokens (single) and ~U[32,554] tokens (batch). Encoder caches are cleared before
+    every timed batch pass so no pass is served from them."""
+    words = synth.corpus_words()
+    r = np.random.default_rng(21)
+
+    def row(n_words, n_opts):
+        pick = lambda n: " ".join(words[int(i)] for i in r.integers(0, len(words), n))
+        return dict(state=pick(n_words), question=pick(6), options=[pick(3) for _ in range(n_opts)])
+
+    # words per token of this tokenizer on such rows, to size them
+    probe = [row(200, 4) for _ in range(8)]
+    per_word = np.mean([len(te.encoder.encode(p)["ids"]) for p in probe]) / 200.0
+    # states sized for ~U[140,180] tokens per row in all (question and options take ~8) and, for the batch,
+    # the published mean of ~293 tokens per row
+    singles = [row(int(n / per_word), int(r.integers(2, 9))) for n in r.integers(126, 167, 320)]
+    batch = [row(int(n / per_word), int(r.integers(2, 9))) for n in r.integers(38, 561, 2000)]
+    tok = [len(te.encoder.encode(x)["ids"]) for x in singles]
+    btok = sum(len(te.encoder.encode(x)["ids"]) for x in batch)
+    te.encoder.clear_cache()
+    for x in singles[:20]:
+        te.logits([x])
+    lat = []
+    for x in singles[20:]:
+        t = time.perf_counter()
+        te.logits([x])
+        lat.append((time.perf_counter() - t) * 1e3)
+    lat.sort()
+    passes = []
+    for _ in range(3):
+        te.encoder.clear_cache()
+        passes.append(_timed(lambda: te.logits(batch)))
+    best = min(passes)
+    return dict(single=dict(n=len(lat), mean_tokens=round(float(np.mean(tok[20:])), 1),
+                            mean_ms=round(float(np.mean(lat)), 3), p50_ms=round(lat[len(lat) // 2], 3),
+                            p99_ms=round(lat[int(0.99 * (len(lat) - 1))], 3)),
+                batch=dict(n=len(batch), tokens=int(btok), best_s=round(best, 4), rows_per_s=round(len(batch) / best, 1)),
+                tokenizer="synthetic byte-level BPE (vocab 500), tokenizers library via Python callback")
 
 
 def _timed(fn):

@@ -58,6 +58,14 @@ typedef struct jt_tokenizer {
     void* ctx;
     int (*encode)(void* ctx, const char* text, size_t len, uint32_t* ids, size_t capacity, size_t* count);
     int (*token_to_id)(void* ctx, const char* name, uint32_t* id);
+    /* Optional (null: `encode` per text).  Tokenizes n texts in one call, as
+     * the reference's parallel row encoding does (rayon over rows with
+     * Tokenizer::encode_fast, src/engine.rs:183-188, src/encode.rs:110):
+     * counts[i] receives text i's token count and *ids the concatenated ids,
+     * in callback-owned memory that stays valid until the calling thread's
+     * next encode_batch call on this ctx.  Same ids as `encode`. */
+    int (*encode_batch)(void* ctx, size_t n, const char* const* texts, const size_t* lens, size_t* counts,
+                        const uint32_t** ids);
 } jt_tokenizer;
 
 /* The encoder fields of `EngineOptions` (src/engine.rs:34-65). */

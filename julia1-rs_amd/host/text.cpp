@@ -15,6 +15,7 @@
 #include <mutex>
 #include <string>
 #include <unordered_map>
+#include <unordered_set>
 #include <utility>
 #include <vector>
 
@@ -523,8 +524,15 @@ struct jt_encoder {
 
     jt_encoder(size_t tc, size_t ec) : tokens(tc), encodings(ec) {}
 
+    // Token ids already produced for this call by a batch tokenization (encode_many).
+    using Pre = std::unordered_map<std::string, Ids>;
+
     // Encoder::tokenize (src/encode.rs:104-116)
-    Ids tokenize(const std::string& text) {
+    Ids tokenize(const std::string& text, const Pre* pre = nullptr) {
+        if (pre) {
+            auto it = pre->find(text);
+            if (it != pre->end()) return it->second;
+        }
         Ids hit;
         if (tokens.get(text, hit)) return hit;
         std::vector<uint32_t> ids(std::max<size_t>(64, text.size() + 8));
@@ -545,22 +553,28 @@ struct jt_encoder {
 
     // Encoder::encode (src/encode.rs:118-135): the cache key covers the
     // rendered state, question, options, qtype and whether the state is text.
+    static std::string cache_key(const Request& row, const std::string& state) {
+        std::string key;
+        auto field = [&](const std::string& s) {
+            key += std::to_string(s.size());
+            key += ':';
+            key += s;
+        };
+        field(state);
+        field(row.question);
+        key += std::to_string(row.options.size());
+        key += '|';
+        for (const auto& o : row.options) field(o);
+        key += kQNames[row.qtype];
+        key += row.text ? 't' : 'j';
+        return key;
+    }
+
     std::shared_ptr<const Encoded> encode(const Request& row) {
         const std::string state = row.render();
         std::string key;
         if (encodings.enabled()) {
-            auto field = [&](const std::string& s) {
-                key += std::to_string(s.size());
-                key += ':';
-                key += s;
-            };
-            field(state);
-            field(row.question);
-            key += std::to_string(row.options.size());
-            key += '|';
-            for (const auto& o : row.options) field(o);
-            key += kQNames[row.qtype];
-            key += row.text ? 't' : 'j';
+            key = cache_key(row, state);
             std::shared_ptr<const Encoded> hit;
             if (encodings.get(key, hit)) return hit;
         }
@@ -569,20 +583,99 @@ struct jt_encoder {
         return e;
     }
 
+    // Engine::encode's row encoding (src/engine.rs:183-188): the reference
+    // encodes rows in parallel with Tokenizer::encode_fast.  Here, with a
+    // batch tokenizer and more than one row, every distinct segment the
+    // uncached rows need that the token cache lacks is tokenized in one call
+    // (the tokenizer may run it in parallel), then each row is assembled as
+    // encode() would; the results are the same ids.  A single row keeps the
+    // per-text calls: its few segments do not repay a parallel dispatch.
+    std::vector<std::shared_ptr<const Encoded>> encode_many(const std::vector<Request>& rows) {
+        std::vector<std::shared_ptr<const Encoded>> out(rows.size());
+        if (!tok.encode_batch || rows.size() < 2) {
+            for (size_t i = 0; i < rows.size(); ++i) out[i] = encode(rows[i]);
+            return out;
+        }
+        std::vector<std::string> states(rows.size()), keys(rows.size());
+        std::vector<size_t> miss;
+        for (size_t i = 0; i < rows.size(); ++i) {
+            states[i] = rows[i].render();
+            if (encodings.enabled()) {
+                keys[i] = cache_key(rows[i], states[i]);
+                if (encodings.get(keys[i], out[i])) continue;
+            }
+            miss.push_back(i);
+        }
+        std::vector<std::string> texts;
+        std::unordered_set<std::string> seen;
+        for (size_t i : miss)
+            for (std::string& t : segments(rows[i], states[i])) {
+                Ids hit;
+                if (seen.count(t) || tokens.get(t, hit)) continue;
+                seen.insert(t);
+                texts.push_back(std::move(t));
+            }
+        const Pre pre = tokenize_batch(texts);
+        for (size_t i : miss) {
+            out[i] = std::make_shared<const Encoded>(sequence(states[i], rows[i], &pre));
+            if (encodings.enabled()) encodings.put(keys[i], out[i]);
+        }
+        return out;
+    }
+
+    // One encode_batch call for `texts`; the results also enter the token cache.
+    Pre tokenize_batch(const std::vector<std::string>& texts) {
+        Pre pre;
+        if (texts.empty()) return pre;
+        std::vector<const char*> ptrs;
+        std::vector<size_t> lens, counts(texts.size(), 0);
+        for (const auto& t : texts) {
+            ptrs.push_back(t.data());
+            lens.push_back(t.size());
+        }
+        const uint32_t* ids = nullptr;
+        if (tok.encode_batch(tok.ctx, texts.size(), ptrs.data(), lens.data(), counts.data(), &ids) != 0)
+            invalid("tokenizer failed");
+        size_t total = 0;
+        for (size_t c : counts) total += c;
+        if (total && !ids) invalid("tokenizer failed");
+        size_t off = 0;
+        for (size_t i = 0; i < texts.size(); ++i) {
+            auto v = std::make_shared<const std::vector<uint32_t>>(ids + off, ids + off + counts[i]);
+            off += counts[i];
+            tokens.put(texts[i], v);
+            pre.emplace(texts[i], std::move(v));
+        }
+        return pre;
+    }
+
+    // The texts Encoder::sequence tokenizes for a row: the question head,
+    // each option (with its leading space) and the state, marker text blanked.
+    std::string clean(const std::string& t) const { return replace_all(t, mask_token, " "); }
+    std::string head_text(const Request& row) const {
+        return std::string(kQNames[row.qtype]) + " question: " + clean(row.question);
+    }
+    std::string option_text(const std::string& o) const { return " " + clean(o); }
+    std::vector<std::string> segments(const Request& row, const std::string& state) const {
+        std::vector<std::string> out{head_text(row)};
+        for (const auto& o : row.options) out.push_back(option_text(o));
+        out.push_back(clean(state));
+        return out;
+    }
+
     // Encoder::sequence (src/encode.rs:137-195): [CLS] head [SEP] (<mask>
     // option)* [SEP] state [SEP], with the head/option budget and the state
     // truncated to max_length.
-    Encoded sequence(const std::string& state, const Request& row) {
+    Encoded sequence(const std::string& state, const Request& row, const Pre* pre = nullptr) {
         const std::string& mask = mask_token;
         if (strict) {
             bool found = state.find(mask) != std::string::npos || row.question.find(mask) != std::string::npos;
             for (const auto& o : row.options) found |= o.find(mask) != std::string::npos;
             if (found) invalid("Reserved model marker in request");
         }
-        auto clean = [&](const std::string& t) { return replace_all(t, mask, " "); };
-        const Ids head = tokenize(std::string(kQNames[row.qtype]) + " question: " + clean(row.question));
+        const Ids head = tokenize(head_text(row), pre);
         std::vector<Ids> option_ids;
-        for (const auto& o : row.options) option_ids.push_back(tokenize(" " + clean(o)));
+        for (const auto& o : row.options) option_ids.push_back(tokenize(option_text(o), pre));
         if (strict)
             for (const auto& x : option_ids)
                 if (x->size() > kOptionTokens) invalid("Option exceeds 48-token model contract");
@@ -625,7 +718,7 @@ struct jt_encoder {
             e.ids.insert(e.ids.end(), o.begin(), o.end());
         }
         e.ids.push_back(sep_id);
-        const Ids state_ids = tokenize(clean(state));
+        const Ids state_ids = tokenize(clean(state), pre);
         const int64_t room = (int64_t)max_length - (int64_t)e.ids.size() - 1;
         if (room < 1) invalid("Question/options exceed sequence budget; shorten descriptions");
         if (strict && (int64_t)state_ids->size() > room) invalid("Game state exceeds lossless context budget");
@@ -665,9 +758,7 @@ struct jt_scorer {
         }
         // Engine::encode: validate every row, then encode every row, before inference.
         for (size_t i = 0; i < rows.size(); ++i) request_validate(rows[i], i + 1);
-        std::vector<std::shared_ptr<const Encoded>> enc;
-        enc.reserve(rows.size());
-        for (const auto& r : rows) enc.push_back(encoder->encode(r));
+        const std::vector<std::shared_ptr<const Encoded>> enc = encoder->encode_many(rows);
         std::vector<uint32_t> ids, markers;
         std::vector<size_t> id_off{0}, mk_off{0};
         std::vector<uint8_t> qt;
@@ -1156,8 +1247,7 @@ int jt_encoding_info(jt_encoder* e, const char* jsonl, size_t len, char** out) {
         if (!e->strict) invalid("Lossless encoding audit requires strict_encoding=True");
         const auto rows = parse_rows(jsonl, len);
         for (size_t i = 0; i < rows.size(); ++i) request_validate(rows[i], i + 1);
-        std::vector<std::shared_ptr<const Encoded>> enc;
-        for (const auto& r : rows) enc.push_back(e->encode(r));
+        const std::vector<std::shared_ptr<const Encoded>> enc = e->encode_many(rows);
         std::string o = "[";
         for (size_t i = 0; i < enc.size(); ++i) {
             if (i) o += ", ";

@@ -132,6 +132,11 @@ _WORDS = ("x", "the", "a", "to", "of", "and", "in", "is", "it", "you", "that", "
           "context", "plain", "text", "word", "number", "largest", "approve", "review", "human", "run", "value")
 
 
+def corpus_words() -> tuple:
+    """The words of the synthetic tokenizer's training corpus (for text rows it encodes compactly)."""
+    return _WORDS
+
+
 def train_tokenizer(vocab_size: int = 500):
     """A byte-level BPE `tokenizers.Tokenizer` trained on a seeded synthetic corpus: the stand-in for a
     checkpoint's tokenizer.json (absent here).  " x" is a single token, as in the Julia-1 tokenizer

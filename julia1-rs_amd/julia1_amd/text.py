@@ -14,8 +14,10 @@ is handed to the C++ encoder as a callback.
 from __future__ import annotations
 
 import ctypes as C
+import itertools
 import json
 import os
+import threading
 
 import numpy as np
 
@@ -25,11 +27,13 @@ from . import hip
 ENCODE_FN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_void_p, C.c_size_t, C.POINTER(C.c_uint32), C.c_size_t,
                         C.POINTER(C.c_size_t))
 TOKEN_FN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_char_p, C.POINTER(C.c_uint32))
+BATCH_FN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_size_t, C.POINTER(C.c_void_p), C.POINTER(C.c_size_t),
+                       C.POINTER(C.c_size_t), C.POINTER(C.POINTER(C.c_uint32)))
 LOGITS_FN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p)
 
 
 class JtTokenizer(C.Structure):
-    _fields_ = [("ctx", C.c_void_p), ("encode", ENCODE_FN), ("token_to_id", TOKEN_FN)]
+    _fields_ = [("ctx", C.c_void_p), ("encode", ENCODE_FN), ("token_to_id", TOKEN_FN), ("encode_batch", BATCH_FN)]
 
 
 class JtEncoderOptions(C.Structure):
@@ -130,13 +134,18 @@ class Tokenizer:
     """A `tokenizers.Tokenizer` (tokenizer.json) behind the jt_tokenizer callbacks, with truncation and
     padding off (src/encode.rs:67-68)."""
 
-    def __init__(self, tok):
+    def __init__(self, tok, batch: bool = True):
         tok.no_truncation()
         tok.no_padding()
         self.tok = tok
         self._encode = ENCODE_FN(self._encode_cb)
         self._token = TOKEN_FN(self._token_cb)
-        self.struct = JtTokenizer(None, self._encode, self._token)
+        # Batch tokenization (the library's parallel encode_batch_fast: ids without offsets, as the
+        # reference's encode_fast); the ids handed back stay alive per thread until its next call.
+        self._fast = getattr(tok, "encode_batch_fast", None) or tok.encode_batch
+        self._kept = threading.local()
+        self._batch = BATCH_FN(self._batch_cb) if batch else BATCH_FN()
+        self.struct = JtTokenizer(None, self._encode, self._token, self._batch)
 
     @staticmethod
     def from_file(path: str) -> "Tokenizer":
@@ -151,6 +160,19 @@ class Tokenizer:
             if k:
                 a = np.asarray(out[:k], dtype=np.uint32)
                 C.memmove(ids, a.ctypes.data, 4 * k)
+            return 0
+        except Exception:
+            return 1
+
+    def _batch_cb(self, ctx, n, texts, lens, counts, ids_out):
+        try:
+            encs = self._fast([C.string_at(texts[i], lens[i]).decode("utf-8") for i in range(n)],
+                              add_special_tokens=False)
+            for i, e in enumerate(encs):
+                counts[i] = len(e.ids)
+            flat = np.fromiter(itertools.chain.from_iterable(e.ids for e in encs), dtype=np.uint32)
+            self._kept.ids = flat
+            ids_out[0] = flat.ctypes.data_as(C.POINTER(C.c_uint32))
             return 0
         except Exception:
             return 1

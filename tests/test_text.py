@@ -463,6 +463,38 @@ def test_full_budget_and_strict_overflow(tok):
         enc.encode(row(fill(8193 - overhead)))
 
 
+def test_batch_tokenization_matches_per_text(tok):
+    """Engine::encode (src/engine.rs:183-188) encodes rows in parallel with encode_fast; here every distinct
+    segment the uncached rows need goes to one batch-tokenizer call. The encodings equal those of per-text
+    calls, and rows or segments already cached are not tokenized again."""
+    per = text.Encoder(text.Tokenizer(tok.tok, batch=False), CFG, 1024, head_length=256, strict=True)
+    rng = random.Random(5)
+    rows = []
+    while len(rows) < 40:
+        r = _random_row(rng, allow_mask=False, option_words=12)
+        try:
+            per.encode(r)
+        except hip.HipError:
+            continue
+        rows.append(r)
+    rows += rows[:5]  # repeated rows
+    bt = text.Tokenizer(tok.tok)
+    calls, fast = [], bt._fast
+    bt._fast = lambda texts, **kw: (calls.append(list(texts)), fast(texts, **kw))[1]  # noqa: E731
+    bat = text.Encoder(bt, CFG, 1024, head_length=256, strict=True)
+    assert bat.encoding_info(rows) == per.encoding_info(rows)
+    assert len(calls) == 1 and len(set(calls[0])) == len(calls[0])
+    assert bat.encoding_info(rows) == per.encoding_info(rows) and len(calls) == 1  # all cached now
+    for r in rows:
+        assert bat.encode(r) == per.encode(r)
+    # without caches every row is assembled from the one batch call
+    calls.clear()
+    nocache = text.Encoder(bt, CFG, 1024, head_length=256, strict=True, token_cache=0, encoding_cache=0)
+    assert nocache.encoding_info(rows) == per.encoding_info(rows) and len(calls) == 1
+    # a single row keeps the per-text calls
+    assert nocache.encoding_info(rows[:1]) == per.encoding_info(rows[:1]) and len(calls) == 1
+
+
 class CountingTokenizer(text.Tokenizer):
     calls = 0
 
