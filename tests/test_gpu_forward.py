@@ -201,6 +201,33 @@ def test_collect_waits_without_blocking_submit(tiny):
     assert np.array_equal(out["a"], r1) and np.array_equal(got2, r2)
 
 
+def test_edge_batches(tiny):
+    """Batches at the edges of Batch::new (src/model.rs:127-147): no sequences; sequences without markers
+    among ones with markers; markers on the first and last token; a one-token sequence marked; a sequence
+    whose every token is a marker; a qtype of each kind. Scores match the oracle, and a batch without markers
+    returns no scores without running anything."""
+    ws, gpu, orc = tiny
+    v = ws.cfg.vocab
+    r = np.random.default_rng(3)
+    empty = abi.Batch.from_items([])
+    assert gpu.forward(empty).size == 0 and orc.forward(empty).size == 0
+    unmarked = abi.Batch.from_items([(r.integers(0, v, 30), [], 0), (r.integers(0, v, 7), [], 2)])
+    assert gpu.forward(unmarked).size == 0
+    items = [(r.integers(0, v, 50), [0, 49], 0), (r.integers(0, v, 20), [], 1), (r.integers(0, v, 1), [0], 2),
+             (r.integers(0, v, 9), list(range(9)), 1), (r.integers(0, v, ws.cfg.max_positions), [], 0),
+             (r.integers(0, v, 129), [1, 64, 128], 2)]
+    b = abi.Batch.from_items(items)
+    got, ref = gpu.forward(b), orc.forward(b)
+    s = parity(b, got, ref)
+    print(s)
+    assert s["max_dlogit"] <= 2e-2 and s["max_dsoftmax"] <= 1e-2, s
+    # argmax wherever the oracle's top two differ by more than bf16 round-off (random weights give near-ties)
+    for g, r in zip(b.split_scores(got), b.split_scores(ref)):
+        if r.size > 1 and np.diff(np.sort(r))[-1] > 1e-3:
+            assert np.argmax(g) == np.argmax(r)
+    assert [g.size for g in b.split_scores(got)] == [2, 0, 1, 9, 0, 3]
+
+
 def test_invalid_batches_rejected(tiny):
     ws, gpu, _ = tiny
     b = synth.make_batch([10, 5], [2, 1], ws.cfg.vocab, 1)
