@@ -105,6 +105,38 @@ def test_gemm_geglu(rows, inter, k):
     assert np.all(np.abs(oracle.linear_geglu(x, wi) - expect) <= 1e-5 * (1 + np.abs(expect)))
 
 
+@pytest.mark.parametrize("n,k,epi", [(2304, 768, abi.EPI_STORE_BF16), (768, 768, abi.EPI_RESID_F32),
+                                     (2304, 768, abi.EPI_GEGLU_BF16), (768, 1152, abi.EPI_RESID_F32)])
+def test_gemm_sweep_shapes_full_size(n, k, epi):
+    """The GEMM sweep's four shapes (configs[2]: Wqkv, attention-out + residual, Wi + GEGLU, MLP-out +
+    residual) at M = 16384, where the persistent kernel walks several tiles per workgroup, against a torch
+    FP32 product of the same bf16 operands on the GPU (FP32 accumulation order may differ; the bf16 outputs
+    round once)."""
+    M = 16384
+    g = torch.Generator(device="cuda").manual_seed(n + k + epi)
+    x = torch.randn(M, k, device="cuda", generator=g).to(BF16)
+    w = (torch.randn(n, k, device="cuda", generator=g) * 0.02).to(BF16)
+    prod = x.float() @ w.float().T
+    if epi == abi.EPI_RESID_F32:
+        base = torch.randn(M, n, device="cuda", generator=g)
+        out = base.clone()
+        hip.op_gemm(epi, x, w, out)
+        torch.cuda.synchronize()
+        assert (out - (base + prod)).abs().max().item() < 1e-4
+        return
+    if epi == abi.EPI_GEGLU_BF16:
+        inter = n // 2
+        expect = torch.nn.functional.gelu(prod[:, :inter]) * prod[:, inter:]
+        wk = dev(hip.interleave_geglu(w.float().cpu().numpy()), BF16)
+    else:
+        expect, wk = prod, w
+    out = torch.zeros(M, expect.shape[1], dtype=BF16, device="cuda")
+    hip.op_gemm(epi, x, wk, out)
+    torch.cuda.synchronize()
+    d = (out.float() - expect).abs()
+    assert bool((d <= 4e-3 * expect.abs() + 1e-5).all()), d.max().item()
+
+
 @pytest.mark.parametrize("theta", [10000.0, 160000.0])
 def test_gemm_rope(theta):
     r = rng(6)
