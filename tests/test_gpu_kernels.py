@@ -365,6 +365,32 @@ def test_attention_varlen(window, qt):
     assert np.abs(orc - expect).max() < 1e-4
 
 
+@pytest.mark.parametrize("window", [-1, 64])
+def test_attention_full_length_8192(window):
+    """One 8192-token sequence with the ModernBERT-base heads, global and sliding-window, in the
+    backend's 128-query tiles, against softmax(0.125·QKᵀ + mask)·V in FP32 on the GPU, head by head."""
+    L, heads = 8192, 12
+    h = heads * 64
+    g = torch.Generator(device="cuda").manual_seed(8192 + window)
+    qkv = torch.randn(L, 3 * h, device="cuda", generator=g).to(BF16)
+    tiles = dev(np.array(_tiles([L], 128), dtype=np.int32))
+    out = torch.zeros(L, h, dtype=BF16, device="cuda")
+    hip.op_attention(qkv, 3 * h, qkv[:, h:], qkv[:, 2 * h:], 3 * h, out, h, tiles, heads, window)
+    pos = torch.arange(L, device="cuda")
+    worst = 0.0
+    for hh in range(heads):
+        q = qkv[:, hh * 64:(hh + 1) * 64].float()
+        k = qkv[:, h + hh * 64:h + (hh + 1) * 64].float()
+        v = qkv[:, 2 * h + hh * 64:2 * h + (hh + 1) * 64].float()
+        s = 0.125 * (q @ k.T.contiguous())
+        if window >= 0:
+            s = s.masked_fill((pos[:, None] - pos[None, :]).abs() > window, float("-inf"))
+        ref = torch.softmax(s, dim=1) @ v
+        worst = max(worst, (out[:, hh * 64:(hh + 1) * 64].float() - ref).abs().max().item())
+        del s, ref
+    assert worst < 2e-2, worst
+
+
 def test_attention_marker_queries():
     """Queries from a separate buffer (the marker-only head layer) against full keys."""
     r = rng(10)
