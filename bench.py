@@ -233,6 +233,9 @@ def main():
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="also run 3 device-to-device copies of MIB MiB (the known-size kernel that "
                          "calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
+    ap.add_argument("--protocol-only", action="store_true",
+                    help="run only the reference's own bench protocol on the Julia-1 shape (token ids and text "
+                         "legs) and print its JSON, e.g. to profile small requests")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -244,6 +247,11 @@ def main():
     import numpy as np
     import torch
     from julia1_amd import abi, hip, synth
+
+    if args.protocol_only:
+        from julia1_amd import engine
+        print(json.dumps({"reference_protocol": reference_protocol(np, synth, engine)}), flush=True)
+        return
 
     t0 = time.time()
     cfg = synth.model_config("modernbert-base")
