@@ -261,6 +261,14 @@ void jh_rope_table(float theta, uint32_t head_dim, uint32_t positions, float* co
 int jh_debug_tokens(jh_model* model, uint32_t* ids_out, uint32_t* pos_out, size_t tokens);
 int jh_debug_encode(jh_model* model, uint32_t layers, float* x_out, size_t tokens);
 
+/*
+ * Test hook: make every later workspace growth fail with JH_ERR_ALLOC once
+ * its device buffers would exceed `bytes` (0 = no limit), part way through
+ * reallocating them, as a failing hipMalloc would.  The model stays usable:
+ * the next batch that fits regrows the workspace.  No reference counterpart.
+ */
+int jh_debug_workspace_limit(jh_model* model, size_t bytes);
+
 #ifdef __cplusplus
 }
 #endif

@@ -196,6 +196,8 @@ struct jh_model {
     bool use_graph = true;
     // split-K GEMMs for outputs with too few tiles (see jh_set_splitk)
     bool use_splitk = true;
+    // debug limit on the bytes of one workspace growth (0 = none; jh_debug_workspace_limit)
+    size_t ws_limit = 0;
     std::string name;
     // attention (query, key) pairs of the staged batch, for algorithmic FLOPs
     double pairs_global = 0, pairs_local = 0, pairs_marker = 0;
@@ -250,7 +252,11 @@ struct jh_model {
 
     // Grows the workspace and the metadata buffers of `slot`.  Submitted
     // forwards may still be running on the old buffers, so growth waits for
-    // the stream before it frees them.
+    // the stream before it frees them.  Before anything is freed the recorded
+    // capacities drop to zero and the generation moves on, so if an
+    // allocation fails part way (JH_ERR_ALLOC) no later forward, graph replay
+    // or profiling replay can touch a freed or missing buffer: the next batch
+    // regrows everything (src/cuda/mod.rs:286-311 clears its buffers the same way).
     void ensure_workspace(size_t t, size_t m, int slot, size_t meta_len) {
         MetaSlot& ms = slots[slot];
         if (t > cap_t || m > cap_m || meta_len > ms.cap) HIP_CHECK(hipStreamSynchronize(stream));
@@ -258,32 +264,40 @@ struct jh_model {
             size_t ct = 1024, cm_ = 256;
             while (ct < std::max(t, cap_t)) ct <<= 1;
             while (cm_ < std::max(m, cap_m)) cm_ <<= 1;
-            size_t H = h, wide = std::max<size_t>(inter, ff);
-            x.alloc(ct * H * 4);
-            xn.alloc(ct * H * 2);
-            qkv.alloc(ct * 3 * H * 2);
-            ctx.alloc(ct * H * 2);
-            hbuf.alloc(ct * wide * 2);
-            y.alloc(cm_ * H * 4);
-            yn.alloc(cm_ * H * 2);
-            qm.alloc(cm_ * H * 2);
-            this->cm.alloc(cm_ * H * 2);
-            hm.alloc(cm_ * ff * 2);
-            z.alloc(cm_ * H * 4);
-            scores.alloc(cm_ * 4);
+            cap_t = cap_m = 0;
+            ++ws_gen;
+            size_t H = h, wide = std::max<size_t>(inter, ff), grown = 0;
+            auto grow = [&](DevBuf& b, size_t bytes) {
+                grown += bytes;
+                if (ws_limit && grown > ws_limit)
+                    throw jh_error(JH_ERR_ALLOC, "workspace of " + std::to_string(grown) + " bytes exceeds the debug limit");
+                b.alloc(bytes);
+            };
+            grow(x, ct * H * 4);
+            grow(xn, ct * H * 2);
+            grow(qkv, ct * 3 * H * 2);
+            grow(ctx, ct * H * 2);
+            grow(hbuf, ct * wide * 2);
+            grow(y, cm_ * H * 4);
+            grow(yn, cm_ * H * 2);
+            grow(qm, cm_ * H * 2);
+            grow(this->cm, cm_ * H * 2);
+            grow(hm, cm_ * ff * 2);
+            grow(z, cm_ * H * 4);
+            grow(scores, cm_ * 4);
             scores_host.alloc(cm_ * 4);
             cap_t = ct;
             cap_m = cm_;
-            ++ws_gen;
         }
         if (meta_len > ms.cap) {
             size_t n = 4096;
             while (n < meta_len) n <<= 1;
+            ms.cap = 0;
+            ms.upload_pending = false;
+            ++ws_gen;
             ms.dev.alloc(n * 4);
             ms.host.alloc(n * 4);
             ms.cap = n;
-            ms.upload_pending = false;
-            ++ws_gen;
         }
         if (!ms.uploaded) HIP_CHECK(hipEventCreateWithFlags(&ms.uploaded, hipEventDisableTiming));
     }
@@ -292,8 +306,10 @@ struct jh_model {
     // upload into metadata slot `slot`; the batch becomes the staged one.
     void stage(int slot, const uint32_t* ids, size_t t, const uint32_t* starts, const uint32_t* lens,
                const uint8_t* qtypes, size_t nseq, const uint32_t* marker_rows, size_t m) {
-        // Recorded replays point into the staged batch's metadata and workspace.
+        // Recorded replays point into the staged batch's metadata and workspace;
+        // a batch that fails to stage leaves none staged.
         for (auto& r : replay) r = nullptr;
+        staged = false;
         if ((t && !ids) || (nseq && (!starts || !lens || !qtypes)) || (m && !marker_rows))
             throw jh_error(JH_ERR_INVALID, "null batch array");
         if (t > (size_t)0x7fffffff || m > (size_t)0x7fffffff) throw jh_error(JH_ERR_INVALID, "batch too large");
@@ -631,16 +647,6 @@ void check_config(const jh_config* c) {
     if (c->half_window > 65535) throw jh_error(JH_ERR_INVALID, "half_window too large");
 }
 
-// Gate/up interleave for the GEGLU epilogue: 64-row block j holds gate rows
-// [32j, 32j+32) then up rows [inter+32j, inter+32j+32).
-void interleave_geglu(const float* wi, size_t inter, size_t k, float* out) {
-    for (size_t j = 0; j < inter / 32; ++j)
-        for (size_t r = 0; r < 32; ++r) {
-            std::memcpy(out + ((64 * j) + r) * k, wi + (32 * j + r) * k, k * sizeof(float));
-            std::memcpy(out + ((64 * j) + 32 + r) * k, wi + (inter + 32 * j + r) * k, k * sizeof(float));
-        }
-}
-
 void build_model(jh_model* m, const jh_config* c, const jh_weights* w, int ordinal) {
     check_config(c);
     if (!w || !w->embedding || !w->layers || !w->head) throw jh_error(JH_ERR_INVALID, "null weights");
@@ -678,7 +684,7 @@ void build_model(jh_model* m, const jh_config* c, const jh_weights* w, int ordin
         L.wo = upload_bf16(s.wo, H * H);
         L.mlp_norm = upload_f32(s.mlp_norm, H);
         if (!s.wi) throw jh_error(JH_ERR_INVALID, "missing Wi");
-        interleave_geglu(s.wi, I, H, wi_tmp.data());
+        jh_op_interleave_geglu(s.wi, I, H, wi_tmp.data());
         L.wi = upload_bf16(wi_tmp.data(), 2 * I * H);
         L.wo2 = upload_bf16(s.wo2, H * I);
         L.global = c->global[l] != 0;
@@ -724,15 +730,25 @@ extern "C" {
 const char* jh_last_error(void) { return jh_error_slot().c_str(); }
 
 void jh_rope_table(float theta, uint32_t head_dim, uint32_t positions, float* cos_out, float* sin_out) {
+    // Column by column, so nothing is allocated (no exception can cross the
+    // C-ABI) and each inverse frequency is still computed once.
     const uint32_t half = head_dim / 2;
-    std::vector<float> inv(half);
-    for (uint32_t i = 0; i < half; ++i) inv[i] = 1.0f / powf(theta, (float)(2 * i) / (float)head_dim);
-    for (uint32_t p = 0; p < positions; ++p)
-        for (uint32_t i = 0; i < half; ++i) {
-            const float f = inv[i] * (float)p;
+    for (uint32_t i = 0; i < half; ++i) {
+        const float inv = 1.0f / powf(theta, (float)(2 * i) / (float)head_dim);
+        for (uint32_t p = 0; p < positions; ++p) {
+            const float f = inv * (float)p;
             cos_out[(size_t)p * half + i] = cosf(f);
             sin_out[(size_t)p * half + i] = sinf(f);
         }
+    }
+}
+
+int jh_debug_workspace_limit(jh_model* model, size_t bytes) {
+    return jh_guarded([&] {
+        if (!model) throw jh_error(JH_ERR_INVALID, "null model");
+        std::lock_guard<std::mutex> g(model->mu);
+        model->ws_limit = bytes;
+    });
 }
 
 int jh_create(const jh_config* config, const jh_weights* weights, int ordinal, jh_model** out) {

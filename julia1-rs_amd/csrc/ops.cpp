@@ -44,6 +44,8 @@ int jh_op_gemm_splitk(int epilogue, const void* x, size_t ldx, const int32_t* ga
     });
 }
 
+// Gate/up interleave for the GEGLU epilogue (also used by jh_create): 64-row
+// block j holds gate rows [32j, 32j+32) then up rows [inter+32j, inter+32j+32).
 void jh_op_interleave_geglu(const float* wi, size_t inter, size_t k, float* out) {
     for (size_t j = 0; j < inter / 32; ++j)
         for (size_t r = 0; r < 32; ++r) {

@@ -262,12 +262,16 @@ private:
             e.name = kv.first;
             e.bf16 = bf16;
             for (const Json& d : shape->arr) {
-                if (!d.is_uint()) invalid("shape");
-                e.shape.push_back((size_t)d.num);
+                uint64_t dim = 0;
+                if (!d.as_u64(dim)) invalid("shape");
+                e.shape.push_back((size_t)dim);
             }
-            if (!offs->arr[0].is_uint() || !offs->arr[1].is_uint()) invalid("data_offsets");
-            size_t a = (size_t)offs->arr[0].num, b = (size_t)offs->arr[1].num;
-            if (!(8 + n + b <= size_ && a <= b)) invalid(kv.first + ": data out of bounds");
+            // Offsets are read from their literal text and checked without
+            // wrap-around: n <= size_ - 8 was checked above (weights.rs slices
+            // the mapping with bounds checks, src/weights.rs:79-89).
+            uint64_t a = 0, b = 0;
+            if (!offs->arr[0].as_u64(a) || !offs->arr[1].as_u64(b)) invalid("data_offsets");
+            if (a > b || b > (uint64_t)(size_ - 8) - n) invalid(kv.first + ": data out of bounds");
             e.begin = 8 + n + a;
             e.end = 8 + n + b;
             tensors_.push_back(std::move(e));

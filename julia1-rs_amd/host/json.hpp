@@ -34,6 +34,20 @@ struct Json {
         return nullptr;
     }
     bool is_uint() const { return kind == Number && integral && num >= 0; }
+    // The exact value of a non-negative integer literal, from its text (the
+    // double loses precision above 2^53); false if it is not one or exceeds 2^64 - 1.
+    bool as_u64(uint64_t& out) const {
+        if (!is_uint() || raw.empty() || raw[0] == '-') return false;
+        uint64_t v = 0;
+        for (char ch : raw) {
+            if (ch < '0' || ch > '9') return false;
+            const uint64_t d = (uint64_t)(ch - '0');
+            if (v > (UINT64_MAX - d) / 10) return false;
+            v = v * 10 + d;
+        }
+        out = v;
+        return true;
+    }
 };
 
 class JsonParser {

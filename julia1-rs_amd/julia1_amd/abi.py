@@ -17,6 +17,11 @@ LIB_DIR = os.path.join(os.path.dirname(_PKG_DIR), "lib")
 LIB_PATH = os.path.join(LIB_DIR, "libjulia1_hip.so")
 
 JH_OK = 0
+JH_ERR_INVALID = 1
+JH_ERR_DEVICE = 2
+JH_ERR_ALLOC = 3
+JH_ERR_NONFINITE = 4
+JH_ERR_INTERNAL = 5
 
 EPI_STORE_BF16 = 0
 EPI_ROPE_BF16 = 1

@@ -19,7 +19,7 @@ EXPORTS = (
     "jh_create", "jh_forward", "jh_forward_padded", "jh_stage", "jh_execute", "jh_scores", "jh_stream", "jh_submit",
     "jh_collect",
     "jh_set_graph", "jh_set_splitk", "jh_name", "jh_destroy", "jh_last_error", "jh_rope_table", "jh_debug_tokens",
-    "jh_debug_encode", "jh_profile", "jh_profile_read", "jh_profile_replay",
+    "jh_debug_encode", "jh_debug_workspace_limit", "jh_profile", "jh_profile_read", "jh_profile_replay",
     "jh_op_gemm", "jh_op_gemm_splitk", "jh_op_interleave_geglu", "jh_op_embed_ln", "jh_op_layer_norm", "jh_op_final_norm",
     "jh_op_gather_f32", "jh_op_scorer", "jh_op_attention",
 )
@@ -65,6 +65,7 @@ def lib():
         L.jh_rope_table.restype = None
         L.jh_debug_tokens.argtypes = [vp, vp, vp, sz]
         L.jh_debug_encode.argtypes = [vp, u32, vp, sz]
+        L.jh_debug_workspace_limit.argtypes = [vp, sz]
         L.jh_profile.argtypes = [vp, C.c_int]
         L.jh_profile_read.argtypes = [vp, vp, sz, C.POINTER(sz)]
         L.jh_profile_replay.argtypes = [vp, C.c_char_p, sz, C.POINTER(C.c_double)]
@@ -178,6 +179,10 @@ class HipModel:
         x = np.zeros((t, self.cfg.hidden), dtype=np.float32)
         check(lib().jh_debug_encode(self.h, layers, _p(x), t))
         return x
+
+    def debug_workspace_limit(self, nbytes: int):
+        """jh_debug_workspace_limit: later workspace growths past `nbytes` fail with JH_ERR_ALLOC (0 = off)."""
+        check(lib().jh_debug_workspace_limit(self.h, nbytes))
 
     def profile(self, on: bool):
         check(lib().jh_profile(self.h, 1 if on else 0))

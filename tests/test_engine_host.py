@@ -93,6 +93,28 @@ def test_safetensors_errors(tiny_ckpt, tmp_path):
             engine.inspect(d)
 
 
+def _raw_header(header: dict, data: bytes = b"") -> bytes:
+    h = json.dumps(header).encode()
+    return struct.pack("<Q", len(h)) + h + data
+
+
+@pytest.mark.parametrize("offsets", [
+    [0, 2 ** 64 - 1],                       # end near 2^64: 8 + n + end would wrap
+    [2 ** 64 - 16, 2 ** 64 - 4],            # both near 2^64
+    [0, 2 ** 64],                           # beyond u64
+    [0, 2 ** 53 + 1],                       # above double precision: must not round into range
+    [12, 4],                                # begin after end
+    [0, 13],                                # one past the data
+])
+def test_safetensors_offsets_out_of_range(tiny_ckpt, tmp_path, offsets):
+    """data_offsets are read exactly from their literal text and bounds-checked without wrap-around
+    (the reference slices the mapping with checked bounds, src/weights.rs:79-89)."""
+    blob = _raw_header({"x": {"dtype": "F32", "shape": [3], "data_offsets": offsets}}, b"\0" * 12)
+    d = _copy_ckpt(tiny_ckpt, str(tmp_path / "o"), weights=blob)
+    with pytest.raises(hip.HipError, match="data out of bounds|data_offsets"):
+        engine.inspect(d)
+
+
 def test_wrong_tensor_shape(tmp_path):
     cfg = synth.model_config("tiny")
     t = synth.make_weights(cfg, seed=2)
