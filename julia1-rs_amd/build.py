@@ -1,10 +1,17 @@
-"""Build libjulia1_hip.so (gfx950) in-tree: julia1-rs_amd/lib/libjulia1_hip.so.
+"""Build the gfx950 HIP library in-tree, as a shared object and as a static
+archive, and a plain-C caller linked against the archive:
+
+    julia1-rs_amd/lib/libjulia1_hip.so   (ctypes: the Python package and tests)
+    julia1-rs_amd/lib/libjulia1_hip.a    (what a Rust build.rs links)
+    julia1-rs_amd/lib/jh_caller          (tests/c_abi/jh_caller.c, C99, against the .a)
 
     python julia1-rs_amd/build.py [--jobs N]
 
-Every source is compiled with hipcc for gfx950 only; packed-FP32 instructions
-are disabled on the device (the host pass warns that it does not know the
-feature, which is harmless).  Objects go to julia1-rs_amd/_build/.
+Every source is compiled with hipcc for gfx950 only (non-relocatable device
+code: each object carries its own code object and registers it at load, so
+the archive links like any C++ library); packed-FP32 instructions are disabled
+on the device (the host pass warns that it does not know the feature, which
+is harmless).  Objects go to julia1-rs_amd/_build/.
 """
 from __future__ import annotations
 
@@ -21,6 +28,10 @@ CSRC = os.path.join(HERE, "csrc")
 HOST = os.path.join(HERE, "host")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "lib", "libjulia1_hip.so")
+ARCHIVE = os.path.join(HERE, "lib", "libjulia1_hip.a")
+CALLER_SRC = os.path.join(ROOT, "tests", "c_abi", "jh_caller.c")
+CALLER = os.path.join(HERE, "lib", "jh_caller")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
@@ -65,7 +76,30 @@ def build(jobs: int | None = None) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}{r.stderr}")
     os.replace(tmp, LIB)
+    build_static(objs)
     return LIB
+
+
+def _run(cmd, what):
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"{what} failed: {' '.join(cmd)}\n{r.stdout}{r.stderr}")
+
+
+def build_static(objs):
+    """libjulia1_hip.a from the same objects, and the C99 caller linked against it with the system
+    C/C++ toolchain plus the HIP runtime (the link a Rust build.rs performs)."""
+    tmp = ARCHIVE + ".tmp"
+    if os.path.exists(tmp):
+        os.remove(tmp)
+    _run(["ar", "rcs", tmp, *objs], "ar")
+    os.replace(tmp, ARCHIVE)
+    obj = os.path.join(BUILD, "jh_caller.o")
+    _run(["gcc", "-std=c99", "-O2", "-Wall", "-Wextra", "-Werror", "-pedantic", f"-I{os.path.join(ROOT, 'include')}",
+          "-c", CALLER_SRC, "-o", obj], "compiling the C caller")
+    _run(["g++", "-o", CALLER + ".tmp", obj, ARCHIVE, f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib"],
+         "linking the C caller against the static library")
+    os.replace(CALLER + ".tmp", CALLER)
 
 
 def clean():

@@ -12,9 +12,10 @@ from dataclasses import dataclass, field
 
 import numpy as np
 
-_PKG_DIR = os.path.dirname(os.path.abspath(__file__))
-LIB_DIR = os.path.join(os.path.dirname(_PKG_DIR), "lib")
-LIB_PATH = os.path.join(LIB_DIR, "libjulia1_hip.so")
+from . import build_paths
+
+LIB_DIR = os.path.dirname(build_paths.SHARED)
+LIB_PATH = build_paths.SHARED
 
 JH_OK = 0
 JH_ERR_INVALID = 1

@@ -328,7 +328,7 @@ def test_failed_workspace_growth_leaves_model_usable(tiny):
     ws, _, orc = tiny
     gpu = hip.HipModel(ws)  # fresh: workspace sized for the first batch
     small = synth.make_batch([40, 17], [3, 2], ws.cfg.vocab, 41)
-    big = synth.make_batch([300] * 8, [4] * 8, ws.cfg.vocab, 42)
+    big = synth.make_batch([200] * 12, [4] * 12, ws.cfg.vocab, 42)
     ref_small, ref_big = orc.forward(small), orc.forward(big)
     first = gpu.forward(small)
     assert np.array_equal(gpu.forward(small), first)  # second time: captured and replayed

@@ -33,6 +33,20 @@ def test_library_exports_every_declared_symbol():
     assert set(text.EXPORTS) <= set(names)
 
 
+def test_static_archive_exports_every_declared_symbol():
+    """libjulia1_hip.a (the archive a Rust build.rs links) defines every function include/*.h declares, and the
+    C99 caller under tests/c_abi was linked against it (not against the shared object)."""
+    import subprocess
+    from julia1_amd import build_paths
+    out = subprocess.run(["nm", "-g", "--defined-only", build_paths.ARCHIVE], capture_output=True, text=True, check=True)
+    defined = set(re.findall(r" T (j[het]_\w+)$", out.stdout, flags=re.M))
+    missing = [n for n in declared_functions() if n not in defined]
+    assert not missing, missing
+    assert os.access(build_paths.CALLER, os.X_OK)
+    deps = subprocess.run(["ldd", build_paths.CALLER], capture_output=True, text=True).stdout
+    assert "libjulia1_hip" not in deps and "libamdhip64" in deps, deps
+
+
 def test_last_error_is_empty_string_initially():
     assert hip.lib().jh_last_error() is not None
 
