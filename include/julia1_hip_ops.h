@@ -66,6 +66,23 @@ int jh_op_gemm_splitk(int epilogue, const void* x, size_t ldx, const int32_t* ga
                       const float* bias, const int32_t* pos, const float* cos_t, const float* sin_t,
                       size_t rope_cols, void* workspace, size_t workspace_bytes, int splits, void* stream);
 
+/*
+ * jh_op_gemm_splitk without the workspace argument: the FP32 partial sums live
+ * in a fixed 16 MiB device array inside the library (one per GPU, held until
+ * the process ends), so the call allocates nothing (no hipMalloc, hipFree or
+ * allocating library call).  For callers that cannot allocate: code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc.
+ * `splits` as jh_op_gemm_splitk: 0 picks the split count that fits the array,
+ * a forced count whose partials (splits x rows x N floats) exceed 16 MiB is
+ * rejected with JH_ERR_INVALID.  Calls that overlap on one GPU (two streams,
+ * or two threads) share the array and race; serialise them.  Results equal
+ * jh_op_gemm_splitk's with the same split count.  No reference counterpart.
+ */
+int jh_op_gemm_splitk_noalloc(int epilogue, const void* x, size_t ldx, const int32_t* gather,
+                              size_t rows, const void* w, size_t n, size_t k, void* out, size_t ldo,
+                              size_t col, const float* bias, const int32_t* pos, const float* cos_t,
+                              const float* sin_t, size_t rope_cols, int splits, void* stream);
+
 /* Reorder a host FP32 Wi [2*inter, k] into the gate/up interleave JH_EPI_GEGLU_BF16 expects. */
 void jh_op_interleave_geglu(const float* wi, size_t inter, size_t k, float* out);
 
