@@ -9,12 +9,20 @@ jh_execute per step).  Workload config1: 32 rows,
 lengths U[64,512] from a seed, 2-20 options per row, packed without padding.
 Weights are random-init N(0, 0.02) of the ModernBERT-base shape.
 
-Prints ONE JSON line.  `value` is real (unpadded) tokens per second.  The
+Prints ONE JSON line.  `value` is real (unpadded) tokens per second over the
+K timed steps, with the batch resident in HBM.  `forward_with_pcie_ms` is the
+median of >= 20 whole jh_forward calls (metadata upload, forward, scores
+download) after 3 warm-ups, and `tokens_per_s_with_pcie` its rate.  The
 `roofline` object is for the kernel class with the largest device time:
-achieved = its algorithmic FLOPs (2·M·N·K) per launch / its mean launch time,
-measured with HIP events on the model's stream over K profiled steps.
-`cpu_baseline` times the FP32 CPU oracle (C++ restatement of the reference's
-src/cpu path) on this host's cores, on the same batch.
+achieved = its algorithmic FLOPs (2·M·N·K) per launch / its mean in-forward
+launch time over K profiled forwards, each launch timed by events stamped at
+its dispatch on the model's stream (the interval rocprofv3 reports);
+`frac_replay` is the same launch replayed back to back.  `traffic` is the HBM
+bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE runs
+(profiles/traffic.md).  `cpu_baseline` times the FP32 CPU oracle (C++
+restatement of the reference's src/cpu path) on this host's cores, on the
+same batch.  `parity_vs_cpu` compares the GPU's logits with the oracle's
+(julia1_amd.parity: |dlogit|, |dsoftmax|, argmax, top-2 gap histogram).
 """
 from __future__ import annotations
 
@@ -53,22 +61,24 @@ def log(*a):
 
 
 def roofline(stat, replay_us=None):
-    """Roofline of one kernel class.  The launch duration is `replay_us` (the class's launch
-    replayed back to back between two events, jh_profile_replay) when given, else the mean of
-    the per-launch event pairs."""
+    """Roofline of one kernel class from its in-forward launches: the mean device time of the class's
+    launches over the profiled forwards, each bracketed by events the runtime stamps at the dispatch itself
+    (hipExtLaunchKernelGGL; the interval rocprofv3 reports).  `replay_us` (the class's first launch replayed
+    back to back, jh_profile_replay: hot caches, no neighbours) is reported beside it as frac_replay."""
     event_us = stat["ms"] / stat["launches"] * 1e3
-    per_launch_ms = (replay_us if replay_us else event_us) * 1e-3
+    per = stat["flops" if stat["name"] in MFMA_CLASSES else "bytes"] / stat["launches"]
     if stat["name"] in MFMA_CLASSES:
-        achieved = stat["flops"] / stat["launches"] / (per_launch_ms * 1e-3) / 1e12
-        return dict(bound="mfma", achieved=round(achieved, 2), peak=PEAK_BF16_TFLOPS, unit="TFLOP/s",
-                    frac=round(achieved / PEAK_BF16_TFLOPS, 4), traffic=None,
-                    kernel=stat["name"], launch_us=round(per_launch_ms * 1e3, 2),
-                    launch_us_events=round(event_us, 2), flops_per_launch=stat["flops"] / stat["launches"])
-    achieved = stat["bytes"] / stat["launches"] / (per_launch_ms * 1e-3) / 1e9
-    return dict(bound="hbm", achieved=round(achieved, 1), peak=PEAK_HBM_GBS, unit="GB/s",
-                frac=round(achieved / PEAK_HBM_GBS, 4), traffic=None, kernel=stat["name"],
-                launch_us=round(per_launch_ms * 1e3, 2), launch_us_events=round(event_us, 2),
-                bytes_per_launch=stat["bytes"] / stat["launches"])
+        peak, unit, scale, bound, key = PEAK_BF16_TFLOPS, "TFLOP/s", 1e12, "mfma", "flops_per_launch"
+    else:
+        peak, unit, scale, bound, key = PEAK_HBM_GBS, "GB/s", 1e9, "hbm", "bytes_per_launch"
+    achieved = per / (event_us * 1e-6) / scale
+    out = dict(bound=bound, achieved=round(achieved, 2), peak=peak, unit=unit, frac=round(achieved / peak, 4),
+               traffic=None, kernel=stat["name"], launch_us=round(event_us, 2), launches=stat["launches"])
+    out[key] = per
+    if replay_us:
+        out["launch_us_replay"] = round(replay_us, 2)
+        out["frac_replay"] = round(per / (replay_us * 1e-6) / scale / peak, 4)
+    return out
 
 
 def committed_traffic(kernel, workload, roof):
@@ -277,11 +287,16 @@ def main():
     value = tokens * args.steps / elapsed
     log(f"{args.workload}: {tokens} tokens, {ms_per_step:.3f} ms/step, {value:,.0f} tokens/s")
 
-    # PCIe-inclusive rate (host batch in, scores out) for reference: jh_forward per step.
-    t1 = time.perf_counter()
-    for _ in range(max(3, args.steps // 4)):
+    # PCIe-inclusive latency (host batch in, scores out): the median of >= 20 jh_forward calls after 3
+    # warm-ups, each one whole forward from the metadata upload to the scores download.
+    for _ in range(3):
         model.forward(batch)
-    fwd_ms = (time.perf_counter() - t1) / max(3, args.steps // 4) * 1e3
+    fwd = []
+    for _ in range(max(20, args.steps)):
+        t1 = time.perf_counter()
+        model.forward(batch)
+        fwd.append((time.perf_counter() - t1) * 1e3)
+    fwd_ms = statistics.median(fwd)
 
     # ---- per-kernel device time: the same K steps, eager with HIP events per launch
     model.profile(True)
@@ -421,9 +436,8 @@ def main():
                    sample=f"{args.workload}: full batch ({tokens} tokens), median of 3 forwards, "
                           f"FP32 C++ restatement of reference src/cpu (AVX-512 8x32 GEMM tile), "
                           f"{threads} OpenMP threads")
-        gs, rs = batch.split_scores(gpu_scores), batch.split_scores(ref)
-        parity = dict(max_dlogit=float(np.abs(gpu_scores - ref).max()),
-                      argmax_agree=sum(int(np.argmax(a) == np.argmax(b)) for a, b in zip(gs, rs)), rows=len(gs))
+        from julia1_amd import parity as par
+        parity = par.report(batch.split_scores(gpu_scores), batch.split_scores(ref))
         log(f"cpu oracle: {med:.2f} s/forward on {threads} threads; parity {parity}")
         if not args.no_extra and threads != 4:
             # The reference CPU path's default thread count (JULIA_CPU_THREADS=4, src/engine.rs:160-162).
@@ -435,18 +449,21 @@ def main():
                 t4.append(time.perf_counter() - tc)
             cpu["value_4_threads"] = round(tokens / statistics.median(t4), 1)
             log(f"cpu oracle: {statistics.median(t4):.2f} s/forward on 4 threads")
-        # configs[0] (one 128-token request) on the same oracle and threads, and the host it ran on.
+        # configs[0] (one 128-token request) on the same oracle and threads, and at the reference CPU path's
+        # default of 4 threads (JULIA_CPU_THREADS, src/engine.rs:160-162); and the host it ran on.
         b0 = synth.workload("config0")
-        orc.forward(b0)
-        t0 = []
-        for _ in range(5):
-            tc = time.perf_counter()
-            orc.forward(b0)
-            t0.append(time.perf_counter() - tc)
-        cpu["config0_ms"] = round(statistics.median(t0) * 1e3, 2)
+        for key, o in (("config0_ms", orc), ("config0_ms_4_threads", oracle.OracleModel(ws, threads=4))):
+            o.forward(b0)
+            t0 = []
+            for _ in range(5):
+                tc = time.perf_counter()
+                o.forward(b0)
+                t0.append(time.perf_counter() - tc)
+            cpu[key] = round(statistics.median(t0) * 1e3, 2)
         cpu["host"] = dict(cpu_model=cpu_model_name(), cpus_visible=len(os.sched_getaffinity(0)),
                            cpus_total=os.cpu_count())
-        log(f"cpu oracle: config0 {cpu['config0_ms']} ms/forward on {threads} threads; host {cpu['host']}")
+        log(f"cpu oracle: config0 {cpu['config0_ms']} ms/forward on {threads} threads, "
+            f"{cpu['config0_ms_4_threads']} ms on 4; host {cpu['host']}")
 
     out = {
         "metric": METRIC, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
@@ -461,6 +478,7 @@ def main():
         "gemm_mfma_util_pct": round(gemm_util, 2),
         "profiled_ms_per_step": round(prof_step_ms, 4),
         "forward_with_pcie_ms": round(fwd_ms, 4),
+        "tokens_per_s_with_pcie": round(tokens / fwd_ms * 1e3, 1),
         "kernels": kern,
         "parity_vs_cpu": parity,
         **extra,
