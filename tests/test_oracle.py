@@ -16,6 +16,7 @@ What pins what:
 Planted mistakes (jo_set_fault) must each fail the check that covers them.
 """
 import ctypes
+import hashlib
 import json
 import math
 import os
@@ -225,6 +226,64 @@ def test_forward_matches_golden(golden):
     enc = oracle.layer_norm(x, golden["t"]["encoder.final_norm.weight"], None, 1e-5)
     assert np.max(np.abs(enc - g["encoder_out"])) < 5e-6
     assert np.max(np.abs(m.forward(b) - g["scores"])) < _golden_tol(g)
+
+
+def test_tiny_layerwise_matches_golden(golden):
+    """The residual stream after the embeddings and after every encoder layer, at every 7th token row, against
+    the reconstruction's layer outputs (forward hooks on ModernBertModel's embeddings and layers)."""
+    m, b, g = golden["model"], golden["b"], golden["g"]
+    rows = g["layer_rows"]
+    for l in range(golden["cfg"].layers + 1):
+        assert np.max(np.abs(m.encode(b, l)[rows] - g["layers"][l])) < 5e-6, l
+
+
+@pytest.fixture(scope="module")
+def base_golden():
+    """configs[0] and configs[1] at the ModernBERT-base shape (22 layers, hidden 768, vocab 50368, head_layers 2)
+    with the bench's weights (seed 0), against the same independent reconstruction (tests/golden/make_golden.py)."""
+    meta = json.load(open(os.path.join(GOLDEN, "base_forward.json")))
+    g = np.load(os.path.join(GOLDEN, "base_forward.npz"))
+    cfg = synth.model_config(meta["shape"])
+    t = synth.make_weights(cfg, seed=meta["weight_seed"])
+    assert synth.weights_sha256(t) == meta["weights_sha256"], "synthetic weight generator drifted"
+    model = oracle.OracleModel(abi.WeightSet(cfg, t), threads=min(8, os.cpu_count() or 1))
+    return dict(cfg=cfg, t=t, g=g, meta=meta, model=model)
+
+
+def test_base_config0_matches_golden(base_golden):
+    bg = base_golden
+    m, g, cfg = bg["model"], bg["g"], bg["cfg"]
+    b = synth.workload("config0")
+    assert hashlib.sha256(b.ids.tobytes()).hexdigest() == bg["meta"]["config0"]["ids_sha256"]
+    rows = g["config0_rows"].astype(np.int64)
+    for i, l in enumerate(bg["meta"]["base_layers"]):
+        assert np.max(np.abs(m.encode(b, l)[rows] - g["config0_layers"][i])) < 2e-5, l
+    enc = oracle.layer_norm(m.encode(b, cfg.layers), bg["t"]["encoder.final_norm.weight"], None, cfg.norm_eps)
+    assert np.max(np.abs(enc[rows] - g["config0_encoder_out"])) < 2e-5
+    assert np.max(np.abs(m.forward(b) - g["config0_scores"])) < 1e-5
+
+
+def test_base_config1_matches_golden(base_golden):
+    bg = base_golden
+    m, g, cfg = bg["model"], bg["g"], bg["cfg"]
+    b = synth.workload("config1")
+    assert hashlib.sha256(b.ids.tobytes()).hexdigest() == bg["meta"]["config1"]["ids_sha256"]
+    assert np.max(np.abs(m.forward(b) - g["config1_scores"])) < 1e-5
+    enc = oracle.layer_norm(m.encode(b, cfg.layers), bg["t"]["encoder.final_norm.weight"], None, cfg.norm_eps)
+    assert np.max(np.abs(enc[g["config1_rows"].astype(np.int64)] - g["config1_encoder_out"])) < 2e-5
+
+
+@pytest.mark.parametrize("fault", [1, 2, 3, 4])
+def test_planted_faults_caught_at_base_shape(base_golden, fault):
+    """1 drop type_emb, 2 RoPE sign, 3 window one wider, 4 skip final norm: each moves configs[0]'s scores far
+    outside the golden tolerance at the full shape too."""
+    b = synth.workload("config0")
+    oracle.set_fault(fault)
+    try:
+        s = base_golden["model"].forward(b)
+    finally:
+        oracle.set_fault(0)
+    assert np.max(np.abs(s - base_golden["g"]["config0_scores"])) > 1e-3
 
 
 @pytest.mark.parametrize("fault", [1, 2, 3, 4])
