@@ -43,6 +43,14 @@ namespace {
 
 constexpr int KT = 64;       // keys per LDS tile
 constexpr int NTHR = 256;   // four waves
+// Lazy rescale threshold (log2 units) and the per-lane sum of 32 p values
+// that proves no p exceeded 2^kLazyLog2 on the fast path: 32 · 2^11 = 2^16.
+constexpr float kLazyLog2 = 11.0f;
+constexpr float kSumMax = 65536.0f;
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
 
 // Chunk swizzles of the 128-byte key rows.  K: 32 consecutive rows read one
 // 16-byte chunk each (as the GEMM operands).  V: a half-wave's transposing
@@ -124,7 +132,8 @@ __global__ __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(4))) void 
     // evaluated as one FMA per score; m is the running max of the raw scores.
     float m = -INFINITY, l = 0.0f;
     const float c = a.scale_log2;
-    const float thr = 8.0f / c;  // raw-score growth of the max that forces a rescale
+    const float thr = kLazyLog2 / c;  // raw-score growth of the max that forces a rescale
+    bool ref_ok = false;              // every lane of the wave has a finite running max
     // Queries of this wave sit at positions [qlo, qlo + 31].
     const int qlo = tile.q_pos + wave * 32;
 
@@ -143,79 +152,108 @@ __global__ __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(4))) void 
         if (it + 1 < ntk) issue(k0 + KT, buf ^ 1);
         const bool skip = !active || (a.window >= 0 && (k0 > qlo + 31 + a.window || k0 + KT - 1 < qlo - a.window));
         if (skip) continue;
-        const uint32_t vtile = lv0 + buf * KT * 64 * 2;  // this tile's V buffer (bytes)
+        lds_u8* const vt = (lds_u8*)&sV[buf][0];  // this tile's V buffer
 
         // Sᵀ for keys [k0, k0+64): two 32-key blocks.
-        f32x16 s[2];
+        auto scores = [&](f32x16(&s)[2]) {
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
+            for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-            for (int e = 0; e < 16; ++e) s[kb][e] = 0.0f;
+                for (int e = 0; e < 16; ++e) s[kb][e] = 0.0f;
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks) {
-                const int r = kb * 32 + lq;
-                bf16x8 kf = *(const bf16x8*)&sK[buf][r * 64 + (((ks * 2 + g) ^ kswz(r)) * 8)];
-                s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], s[kb], 0, 0, 0);
+                for (int ks = 0; ks < 4; ++ks) {
+                    const int r = kb * 32 + lq;
+                    bf16x8 kf = *(const bf16x8*)&sK[buf][r * 64 + (((ks * 2 + g) ^ kswz(r)) * 8)];
+                    s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], s[kb], 0, 0, 0);
+                }
             }
-        }
-        // Masking only where this wave's (query, key) block can hold an invalid
-        // pair (decided per wave, so the branch is uniform): the sequence end,
-        // or a sliding window edge.  Element e of block kb is key
-        // k0 + kb*32 + (e/4)*8 + 4g + e%4.
-        const bool tail = k0 + KT > kend;
-        const bool edge = a.window >= 0 && (k0 < qlo + 31 - a.window || k0 + KT - 1 > qlo + a.window);
-        if (tail || edge) {
-            // Element offset off (key kl + off) is valid iff lo <= off <= hi:
-            // off < kend - kl, and |qpos - kl - off| <= window when windowed.
-            const int kl = k0 + 4 * g;  // key of element 0 in block 0 for this lane
-            int lo = 0, hi = kend - kl - 1;
-            if (a.window >= 0) {
-                lo = max(lo, qpos - kl - a.window);
-                hi = min(hi, qpos - kl + a.window);
-            }
-            // Empty range: move lo far right so off - lo wraps to a huge value.
-            const unsigned span = hi >= lo ? (unsigned)(hi - lo) : 0u;
-            lo = hi >= lo ? lo : 0x40000000;
+        };
+        // P = exp2(c·s - c·m) rounded to bf16, packed in pairs: pp[kb*8 + w]
+        // holds elements 2w, 2w+1 of block kb.  The row sum is taken over the
+        // same bf16 values (v_dot2 with (1, 1)), so numerator and denominator
+        // of the softmax see identical weights.
+        uint32_t pp[16];
+        float ls = 0.0f;
+        auto exps = [&](const f32x16(&s)[2], float mc) {
+            ls = 0.0f;
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const int off = kb * 32 + (e >> 2) * 8 + (e & 3);
-                    const bool ok = (unsigned)(off - lo) <= span;
-                    s[kb][e] = ok ? s[kb][e] : -INFINITY;
+                for (int w = 0; w < 8; ++w) {
+                    const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][2 * w], c, -mc));
+                    const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][2 * w + 1], c, -mc));
+                    pp[kb * 8 + w] = pack2(p0, p1);
+                    ls = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pp[kb * 8 + w]),
+                                                         __builtin_bit_cast(bf16x2, 0x3f803f80u), ls, false);
                 }
+        };
+        // Masking is only needed where this wave's (query, key) block can hold
+        // an invalid pair (decided per wave, so the branch is uniform): the
+        // sequence end, or a sliding window edge.
+        const bool tail = k0 + KT > kend;
+        const bool edge = a.window >= 0 && (k0 < qlo + 31 - a.window || k0 + KT - 1 > qlo + a.window);
+        // Fast path: every key valid and every lane holding a finite running
+        // max.  The max of the tile is then not computed at all: a lane's sum
+        // of p bounds each of its p, so a sum within kSumMax proves no p
+        // exceeded 2^kLazyLog2.  Otherwise (a rare tile whose scores rose past
+        // the running max) the tile is redone on the slow path.
+        bool fast = ref_ok && !(tail || edge);
+        if (fast) {
+            f32x16 s[2];
+            scores(s);
+            exps(s, m * c);
+            fast = __builtin_amdgcn_ballot_w64(!(ls <= kSumMax)) == 0;
         }
-        float mx = -INFINITY;
+        if (!fast) {
+            f32x16 s[2];
+            scores(s);
+            if (tail || edge) {
+                // Element e of block kb is key k0 + kb*32 + (e/4)*8 + 4g + e%4;
+                // element offset off (key kl + off) is valid iff lo <= off <= hi:
+                // off < kend - kl, and |qpos - kl - off| <= window when windowed.
+                const int kl = k0 + 4 * g;  // key of element 0 in block 0 for this lane
+                int lo = 0, hi = kend - kl - 1;
+                if (a.window >= 0) {
+                    lo = max(lo, qpos - kl - a.window);
+                    hi = min(hi, qpos - kl + a.window);
+                }
+                // Empty range: move lo far right so off - lo wraps to a huge value.
+                const unsigned span = hi >= lo ? (unsigned)(hi - lo) : 0u;
+                lo = hi >= lo ? lo : 0x40000000;
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+                for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-            for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[kb][e]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        // Lazy rescale: the running max moves (and O, l are rescaled) only
-        // when some lane's tile max exceeds it by more than 2^8 in p; the
-        // branch is wave-uniform.  Until then p may reach 2^8, which bf16 P
-        // and the FP32 sums carry without loss of relative precision.
-        if (__builtin_amdgcn_ballot_w64(mx > m + thr) != 0) {
-            const float mn = fmaxf(m, mx);
-            const float alpha = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m - mn) * c);
-            l *= alpha;
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                o[0][e] *= alpha;
-                o[1][e] *= alpha;
+                    for (int e = 0; e < 16; ++e) {
+                        const int off = kb * 32 + (e >> 2) * 8 + (e & 3);
+                        const bool ok = (unsigned)(off - lo) <= span;
+                        s[kb][e] = ok ? s[kb][e] : -INFINITY;
+                    }
             }
-            m = mn;
+            float mx = -INFINITY;
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[kb][e]);
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            // Lazy rescale: the running max moves (and O, l are rescaled) only
+            // when some lane's tile max exceeds it by more than kLazyLog2 in
+            // log2 units; the branch is wave-uniform.  Until then p may reach
+            // 2^kLazyLog2, which bf16 P and the FP32 sums carry without loss of
+            // relative precision, and a lane's 32 values sum to at most kSumMax.
+            if (__builtin_amdgcn_ballot_w64(mx > m + thr) != 0) {
+                const float mn = fmaxf(m, mx);
+                const float alpha = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m - mn) * c);
+                l *= alpha;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    o[0][e] *= alpha;
+                    o[1][e] *= alpha;
+                }
+                m = mn;
+            }
+            exps(s, m == -INFINITY ? 0.0f : m * c);
+            ref_ok = __builtin_amdgcn_ballot_w64(m == -INFINITY) == 0;
         }
-        const float mc = m == -INFINITY ? 0.0f : m * c;
-        float ls = 0.0f;
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][e], c, -mc));
-                s[kb][e] = p;
-                ls += p;
-            }
         l += ls;
         // Oᵀ += Vᵀ·Pᵀ over 4 steps of 16 keys.  Step (kb, hb) uses accumulator
         // elements hb*8 .. hb*8+7 of block kb: keys base + 8*(e/4) + 4g + e%4.
@@ -223,34 +261,17 @@ __global__ __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(4))) void 
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
             for (int hb = 0; hb < 2; ++hb) {
-                bf16x8 pf;
-                {
-                    u32x4 r;
-#pragma unroll
-                    for (int w = 0; w < 4; ++w) r[w] = pack2(s[kb][hb * 8 + 2 * w], s[kb][hb * 8 + 2 * w + 1]);
-                    pf = __builtin_bit_cast(bf16x8, r);
-                }
+                const bf16x8 pf = __builtin_bit_cast(
+                    bf16x8, u32x4{pp[kb * 8 + hb * 4], pp[kb * 8 + hb * 4 + 1], pp[kb * 8 + hb * 4 + 2],
+                                  pp[kb * 8 + hb * 4 + 3]});
 #pragma unroll
                 for (int db = 0; db < 2; ++db) {
                     // keys kb*32 + hb*16 + 4g + (0..3) and + 8 + (0..3) of dim db*32 + lq
-                    u32x2 lo, hi;
-                    const uint32_t base = vtile + (db ? voff1 : voff0);
-                    if (kb == 0 && hb == 0) {
-                        asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(lo) : "v"(base));
-                        asm volatile("ds_read_b64_tr_b16 %0, %1 offset:1024" : "=v"(hi) : "v"(base));
-                    } else if (kb == 0) {
-                        asm volatile("ds_read_b64_tr_b16 %0, %1 offset:2048" : "=v"(lo) : "v"(base));
-                        asm volatile("ds_read_b64_tr_b16 %0, %1 offset:3072" : "=v"(hi) : "v"(base));
-                    } else if (hb == 0) {
-                        asm volatile("ds_read_b64_tr_b16 %0, %1 offset:4096" : "=v"(lo) : "v"(base));
-                        asm volatile("ds_read_b64_tr_b16 %0, %1 offset:5120" : "=v"(hi) : "v"(base));
-                    } else {
-                        asm volatile("ds_read_b64_tr_b16 %0, %1 offset:6144" : "=v"(lo) : "v"(base));
-                        asm volatile("ds_read_b64_tr_b16 %0, %1 offset:7168" : "=v"(hi) : "v"(base));
-                    }
-                    // the wait names lo/hi so no use of them is scheduled above it
-                    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(lo), "+v"(hi)::"memory");
-                    bf16x8 vf = __builtin_bit_cast(bf16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+                    const int at = (int)(db ? voff1 : voff0) + kb * 4096 + hb * 2048;
+                    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vt + at));
+                    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vt + at + 1024));
+                    const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+                    const bf16x8 vf = __builtin_bit_cast(bf16x8, u32x4{l2[0], l2[1], h2[0], h2[1]});
                     o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, o[db], 0, 0, 0);
                 }
             }

@@ -366,6 +366,43 @@ def test_attention_varlen(window, qt):
 
 
 @pytest.mark.parametrize("window", [-1, 64])
+def test_attention_rising_scores(window):
+    """Scores that climb along each sequence at several rates (about 2 to 40 log2 units per 64-key tile), so the
+    running max must move again and again after the first tile: every rescale case of the online softmax (a rise
+    within the lazy threshold, just past it, far past it, to where exp2 would overflow without one) against f64."""
+    r = rng(11)
+    heads = 2
+    h = heads * 64
+    lens = [300, 257, 300, 190, 300]
+    rates = [0.15, 0.5, 0.8, 1.3, 3.0]  # beta rise per 64 keys
+    t = sum(lens)
+    q = np.abs(r.standard_normal((t, h))) + 0.5
+    u = np.abs(r.standard_normal(h)) + 0.5
+    k = 0.3 * r.standard_normal((t, h))
+    start = 0
+    for ln, rate in zip(lens, rates):
+        beta = rate * np.arange(ln) / 64.0
+        k[start:start + ln] += beta[:, None] * u[None, :]
+        start += ln
+    v = r.standard_normal((t, h))
+    qkv = bf16_round(np.concatenate([q, k, v], 1).astype(np.float32))
+    q, k, v = qkv[:, :h], qkv[:, h:2 * h], qkv[:, 2 * h:]
+    tiles = _tiles(lens, 128)
+    seqs, start = [], 0
+    for ln in lens:
+        seqs.append((start, ln, start, ln, 0))
+        start += ln
+    expect = _attn_ref64(q, k, v, seqs, heads, window)
+    dq = dev(qkv, BF16)
+    out = torch.zeros(t, h, dtype=BF16, device="cuda")
+    hip.op_attention(dq, 3 * h, dq[:, h:], dq[:, 2 * h:], 3 * h, out, h, dev(np.array(tiles, dtype=np.int32)), heads,
+                     window)
+    got = host(out)
+    assert np.isfinite(got).all()
+    assert np.abs(got - expect).max() < 2e-2, np.abs(got - expect).max()
+
+
+@pytest.mark.parametrize("window", [-1, 64])
 def test_attention_full_length_8192(window):
     """One 8192-token sequence with the ModernBERT-base heads, global and sliding-window, in the
     backend's 128-query tiles, against softmax(0.125·QKᵀ + mask)·V in FP32 on the GPU, head by head."""
