@@ -55,7 +55,8 @@ __device__ constexpr int oswz(int r) {
 // 128/256-byte row segments (8 or 4 rows per instruction) instead of 32
 // scattered 16-byte pieces.
 template <int EPI, int TB = 2>
-__device__ inline void epilogue(const GemmArgs& a, f32x16 (&acc)[2][TB], int fw0, int tw0, int lane, float* stage) {
+__device__ inline void epilogue(const GemmArgs& a, f32x16 (&acc)[2][TB], int fw0, int tw0, int lane, float* stage,
+                                const f32x4* rope_c = nullptr, const f32x4* rope_s = nullptr) {
     constexpr int ROWS = TB * 32;  // staged token rows
     constexpr bool GEGLU = EPI == JH_EPI_GEGLU_BF16;
     constexpr bool F32OUT = EPI == JH_EPI_RESID_F32 || EPI == JH_EPI_BIAS_F32 || EPI == EPI_PARTIAL;
@@ -85,7 +86,7 @@ __device__ inline void epilogue(const GemmArgs& a, f32x16 (&acc)[2][TB], int fw0
         const int tl = j * 32 + lr;
         if constexpr (EPI == JH_EPI_ROPE_BF16) {
             const bool rot = fw0 < a.rope_cols;
-            const long p = rot ? (long)(a.pos[min(tw0 + tl, a.rows - 1)] & 0xffff) * 32 : 0;
+            const long p = rot && !rope_c ? (long)(a.pos[min(tw0 + tl, a.rows - 1)] & 0xffff) * 32 : 0;
 #pragma unroll
             for (int qd = 0; qd < 4; ++qd) {
                 const int d = qd * 8 + g4;
@@ -96,8 +97,8 @@ __device__ inline void epilogue(const GemmArgs& a, f32x16 (&acc)[2][TB], int fw0
                     hi[e] = acc[1][j][qd * 4 + e];
                 }
                 if (rot) {
-                    const f32x4 c = *(const f32x4*)(a.cos_t + p + d);
-                    const f32x4 s = *(const f32x4*)(a.sin_t + p + d);
+                    const f32x4 c = rope_c ? rope_c[j * 4 + qd] : *(const f32x4*)(a.cos_t + p + d);
+                    const f32x4 s = rope_s ? rope_s[j * 4 + qd] : *(const f32x4*)(a.sin_t + p + d);
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         const float x0 = lo[e], x1 = hi[e];
@@ -402,6 +403,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
             coords(nxt, nf0, nt0);
             setup(nf0, nt0, sn);
         }
+        // RoPE epilogue: this lane's cos/sin values for its two tokens are
+        // loaded before the K loop, so their latency (position, then table)
+        // runs under the MFMAs instead of in front of the epilogue.
+        f32x4 rc[EPI == JH_EPI_ROPE_BF16 ? 2 * TB * 4 : 1], rs[EPI == JH_EPI_ROPE_BF16 ? 2 * TB * 4 : 1];
+        if constexpr (EPI == JH_EPI_ROPE_BF16) {
+            if (f0 + wf * 64 < a.rope_cols) {
+#pragma unroll
+                for (int j = 0; j < TB; ++j) {
+                    const long p = (long)(a.pos[min(t0 + wt * 64 + j * 32 + lr, a.rows - 1)] & 0xffff) * 32;
+#pragma unroll
+                    for (int qd = 0; qd < 4; ++qd) {
+                        rc[j * 4 + qd] = *(const f32x4*)(a.cos_t + p + qd * 8 + lg * 4);
+                        rs[j * 4 + qd] = *(const f32x4*)(a.sin_t + p + qd * 8 + lg * 4);
+                    }
+                }
+            }
+        }
         f32x16 acc[FB][TB];
 #pragma unroll
         for (int i = 0; i < FB; ++i)
@@ -456,7 +474,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
 #pragma unroll
             for (int j = 0; j < TB; ++j) {
                 f32x16 part[2][1] = {{acc[0][j]}, {acc[1][j]}};
-                epilogue<EPI, 1>(a, part, f0 + wf * 64, t0 + wt * 64 + j * 32, lane, stg);
+                if constexpr (EPI == JH_EPI_ROPE_BF16)
+                    epilogue<EPI, 1>(a, part, f0 + wf * 64, t0 + wt * 64 + j * 32, lane, stg, rc + j * 4, rs + j * 4);
+                else
+                    epilogue<EPI, 1>(a, part, f0 + wf * 64, t0 + wt * 64 + j * 32, lane, stg);
             }
         }
         if (!has_next) break;
