@@ -338,11 +338,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
 // whose stores (counted by vmcnt too) are then never waited on; the epilogue
 // stages through the last step's buffers, 8 KB per wave, in two 32-row passes.
 // Same products in the same K order as gemm_kernel, so results are identical.
-template <int EPI>
+// BT = 128 or 192 tokens per tile (waves of 64 features x BT/2 tokens): the
+// 128x192 tile moves 17% fewer operand bytes per MFMA in 80 KB of LDS, which
+// still leaves two workgroups per CU.
+template <int EPI, int BT = 128>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void gemm_persist_kernel(GemmArgs a) {
-    constexpr int BF = 128, BT = 128, FB = 2, TB = 2;
-    constexpr int CPR = BK / 8, RPI = 64 / CPR, IPW = BF / RPI / 4, STAGE = BF * BK;
-    __shared__ __align__(1024) bf16_t smem[4 * STAGE];
+    constexpr int BF = 128, FB = 2, TB = BT / 64;
+    constexpr int CPR = BK / 8, RPI = 64 / CPR;
+    constexpr int IPW = BF / RPI / 4, XPW = BT / RPI / 4;  // W / X DMA instructions per wave and stage
+    constexpr int STAGE = BF * BK, XSTAGE = BT * BK;
+    __shared__ __align__(1024) bf16_t smem[2 * STAGE + 2 * XSTAGE];
     bf16_t* const sW = smem;
     bf16_t* const sX = smem + 2 * STAGE;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -358,7 +363,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     };
     struct Src {
         i32x4 rw, rx;
-        uint32_t woff[IPW], xoff[IPW];
+        uint32_t woff[IPW], xoff[XPW];
     };
     auto setup = [&](int f0, int t0, Src& s) {
         s.rw = make_rsrc(a.w + (long)f0 * a.k, (uint64_t)(a.n - f0) * a.k * 2);
@@ -368,22 +373,33 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
             const int lrow = (wave * IPW + j) * RPI + lane / CPR;
             const int c = (lane % CPR) ^ swz(lrow);
             s.woff[j] = (uint32_t)((min(f0 + lrow, a.n - 1) - f0) * a.k + c * 8) * 2;
+        }
+#pragma unroll
+        for (int j = 0; j < XPW; ++j) {
+            const int lrow = (wave * XPW + j) * RPI + lane / CPR;
+            const int c = (lane % CPR) ^ swz(lrow);
             const int t = min(t0 + lrow, a.rows - 1);
             s.xoff[j] = (uint32_t)((t - t0) * (long)a.ldx + c * 8) * 2;
         }
     };
     const uint32_t wl0 = (uint32_t)(uintptr_t)&sW[wave * IPW * 512];
-    const uint32_t xl0 = (uint32_t)(uintptr_t)&sX[wave * IPW * 512];
+    const uint32_t xl0 = (uint32_t)(uintptr_t)&sX[wave * XPW * 512];
     auto issue = [&](const Src& s, int kt, int st) {
         const uint32_t kb = (uint32_t)kt * BK * 2;
 #pragma unroll
-        for (int j = 0; j < IPW; ++j) {
-            const uint32_t lw = __builtin_amdgcn_readfirstlane(wl0 + (st * STAGE + j * 512) * 2);
-            const uint32_t lx = __builtin_amdgcn_readfirstlane(xl0 + (st * STAGE + j * 512) * 2);
-            asm volatile("buffer_load_dwordx4 %1, %2, %3 offen lds" ::"{m0}"(lw), "v"(s.woff[j]), "s"(s.rw), "s"(kb)
-                         : "memory");
-            asm volatile("buffer_load_dwordx4 %1, %2, %3 offen lds" ::"{m0}"(lx), "v"(s.xoff[j]), "s"(s.rx), "s"(kb)
-                         : "memory");
+        for (int j = 0; j < (IPW > XPW ? IPW : XPW); ++j) {
+            if (j < IPW) {
+                const uint32_t lw = __builtin_amdgcn_readfirstlane(wl0 + (st * STAGE + j * 512) * 2);
+                asm volatile("buffer_load_dwordx4 %1, %2, %3 offen lds" ::"{m0}"(lw), "v"(s.woff[j]), "s"(s.rw),
+                             "s"(kb)
+                             : "memory");
+            }
+            if (j < XPW) {
+                const uint32_t lx = __builtin_amdgcn_readfirstlane(xl0 + (st * XSTAGE + j * 512) * 2);
+                asm volatile("buffer_load_dwordx4 %1, %2, %3 offen lds" ::"{m0}"(lx), "v"(s.xoff[j]), "s"(s.rx),
+                             "s"(kb)
+                             : "memory");
+            }
         }
     };
     const int wf = wave & 1, wt = wave >> 1, lr = lane & 31, lg = lane >> 5;
@@ -406,12 +422,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
         // RoPE epilogue: this lane's cos/sin values for its two tokens are
         // loaded before the K loop, so their latency (position, then table)
         // runs under the MFMAs instead of in front of the epilogue.
-        f32x4 rc[EPI == JH_EPI_ROPE_BF16 ? 2 * TB * 4 : 1], rs[EPI == JH_EPI_ROPE_BF16 ? 2 * TB * 4 : 1];
-        if constexpr (EPI == JH_EPI_ROPE_BF16) {
+        // (two tokens only: with three the registers do not fit two waves per SIMD)
+        constexpr bool PRE = EPI == JH_EPI_ROPE_BF16 && TB == 2;
+        f32x4 rc[PRE ? TB * 4 : 1], rs[PRE ? TB * 4 : 1];
+        if constexpr (PRE) {
             if (f0 + wf * 64 < a.rope_cols) {
 #pragma unroll
                 for (int j = 0; j < TB; ++j) {
-                    const long p = (long)(a.pos[min(t0 + wt * 64 + j * 32 + lr, a.rows - 1)] & 0xffff) * 32;
+                    const long p = (long)(a.pos[min(t0 + wt * (BT / 2) + j * 32 + lr, a.rows - 1)] & 0xffff) * 32;
 #pragma unroll
                     for (int qd = 0; qd < 4; ++qd) {
                         rc[j * 4 + qd] = *(const f32x4*)(a.cos_t + p + qd * 8 + lg * 4);
@@ -435,7 +453,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
             if (kt + 1 < KT) issue(sc, kt + 1, st ^ 1);
             else if (has_next) issue(sn, 0, st ^ 1);
             const bf16_t* W = sW + st * STAGE;
-            const bf16_t* X = sX + st * STAGE;
+            const bf16_t* X = sX + st * XSTAGE;
             bf16x8 af[2][FB], bx[2][TB];
             auto load = [&](int ks, int s) {
                 const int c = ks * 2 + lg;
@@ -446,7 +464,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
                 }
 #pragma unroll
                 for (int j = 0; j < TB; ++j) {
-                    const int r = wt * 64 + j * 32 + lr;
+                    const int r = wt * (BT / 2) + j * 32 + lr;
                     bx[s][j] = *(const bf16x8*)&X[r * BK + ((c ^ swz(r)) * 8)];
                 }
             };
@@ -469,15 +487,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
         __syncthreads();  // every wave is done reading the last step's buffers
         if (has_next) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         float* stg = wave < 2 ? (float*)(sW + st_last * STAGE) + wave * 2048
-                              : (float*)(sX + st_last * STAGE) + (wave - 2) * 2048;
+                              : (float*)(sX + st_last * XSTAGE) + (wave - 2) * 2048;
         if (f0 + wf * 64 < a.n) {
 #pragma unroll
             for (int j = 0; j < TB; ++j) {
                 f32x16 part[2][1] = {{acc[0][j]}, {acc[1][j]}};
-                if constexpr (EPI == JH_EPI_ROPE_BF16)
-                    epilogue<EPI, 1>(a, part, f0 + wf * 64, t0 + wt * 64 + j * 32, lane, stg, rc + j * 4, rs + j * 4);
+                const int tw = t0 + wt * (BT / 2) + j * 32;
+                if constexpr (PRE)
+                    epilogue<EPI, 1>(a, part, f0 + wf * 64, tw, lane, stg, rc + j * 4, rs + j * 4);
                 else
-                    epilogue<EPI, 1>(a, part, f0 + wf * 64, t0 + wt * 64 + j * 32, lane, stg);
+                    epilogue<EPI, 1>(a, part, f0 + wf * 64, tw, lane, stg);
             }
         }
         if (!has_next) break;
@@ -758,7 +777,17 @@ void launch_cfg(const GemmArgs& a, hipStream_t s) {
     }
     const int resident = resident_tiles();
     if (a.gather) JH_LAUNCH((gemm_kernel<EPI, true>), dim3(blocks), dim3(256), 0, s, a);
-    else if (blocks > resident) JH_LAUNCH((gemm_persist_kernel<EPI>), dim3(resident), dim3(256), 0, s, a);
+    else if (blocks > resident) {
+        // 128x192 tiles when their rounds of resident workgroups, at 1.5x the
+        // work each, cost no more than the 128x128 tiles' (config1's 9482
+        // tokens: 2 rounds against 3); otherwise the finer tiles quantise better.
+        const long t192 = (long)((a.n + 127) / 128) * ((a.rows + 191) / 192);
+        const long r128 = (blocks + resident - 1) / resident, r192 = (t192 + resident - 1) / resident;
+        if (t192 >= resident && 3 * r192 <= 2 * r128)
+            JH_LAUNCH((gemm_persist_kernel<EPI, 192>), dim3(resident), dim3(256), 0, s, a);
+        else
+            JH_LAUNCH((gemm_persist_kernel<EPI>), dim3(resident), dim3(256), 0, s, a);
+    }
     else JH_LAUNCH((gemm_kernel<EPI, false>), dim3(blocks), dim3(256), 0, s, a);
     HIP_CHECK(hipGetLastError());
 }

@@ -137,6 +137,58 @@ def test_gemm_sweep_shapes_full_size(n, k, epi):
     assert bool((d <= 4e-3 * expect.abs() + 1e-5).all()), d.max().item()
 
 
+@pytest.mark.parametrize("rows,n,k,epi", [(9482, 2304, 768, abi.EPI_STORE_BF16), (9482, 2304, 768, abi.EPI_GEGLU_BF16),
+                                          (9482, 2304, 768, abi.EPI_ROPE_BF16), (9482, 2304, 768, abi.EPI_BIAS_BF16),
+                                          (24000, 768, 768, abi.EPI_RESID_F32)])
+def test_gemm_192_token_tiles(rows, n, k, epi):
+    """Shapes whose persistent GEMM runs 128-feature x 192-token tiles (config1's 9482 tokens: 2 rounds of
+    resident workgroups against 3 for 128x128 tiles; 24000 x 768: 2 against 3), every epilogue family, against a
+    torch FP32 product of the same bf16 operands on the GPU."""
+    g = torch.Generator(device="cuda").manual_seed(rows + n + epi)
+    x = torch.randn(rows, k, device="cuda", generator=g).to(BF16)
+    w = (torch.randn(n, k, device="cuda", generator=g) * 0.02).to(BF16)
+    prod = x.float() @ w.float().T
+    if epi == abi.EPI_RESID_F32:
+        base = torch.randn(rows, n, device="cuda", generator=g)
+        out = base.clone()
+        hip.op_gemm(epi, x, w, out)
+        torch.cuda.synchronize()
+        assert (out - (base + prod)).abs().max().item() < 1e-4
+        return
+    kw, wk, scale = {}, w, None
+    if epi == abi.EPI_GEGLU_BF16:
+        inter = n // 2
+        expect = torch.nn.functional.gelu(prod[:, :inter]) * prod[:, inter:]
+        wk = dev(hip.interleave_geglu(w.float().cpu().numpy()), BF16)
+    elif epi == abi.EPI_BIAS_BF16:
+        bias = torch.randn(n, device="cuda", generator=g) * 0.1
+        expect = prod + bias
+        kw = dict(bias=bias)
+    elif epi == abi.EPI_ROPE_BF16:
+        rc = 2 * n // 3  # q and k rotated, v not
+        pos = torch.randint(0, 512, (rows,), device="cuda", generator=g, dtype=torch.int32)
+        cos, sin = (dev(t) for t in oracle.rope_table(10000.0, 8192))
+        expect = prod.clone()
+        c, sn = cos[pos.long()], sin[pos.long()]
+        scale = prod.abs().clone()
+        for hd in range(0, rc, 64):
+            a, b = prod[:, hd:hd + 32], prod[:, hd + 32:hd + 64]
+            expect[:, hd:hd + 32] = a * c - b * sn
+            expect[:, hd + 32:hd + 64] = b * c + a * sn
+            m = a.abs() + b.abs()
+            scale[:, hd:hd + 32] = m
+            scale[:, hd + 32:hd + 64] = m
+        kw = dict(pos=pos, cos=cos, sin=sin, rope_cols=rc)
+    else:
+        expect = prod
+    out = torch.zeros(rows, expect.shape[1], dtype=BF16, device="cuda")
+    hip.op_gemm(epi, x, wk, out, **kw)
+    torch.cuda.synchronize()
+    d = (out.float() - expect).abs()
+    ref = scale if scale is not None else expect.abs()
+    assert bool((d <= 4e-3 * ref + 1e-5).all()), d.max().item()
+
+
 @pytest.mark.parametrize("theta", [10000.0, 160000.0])
 def test_gemm_rope(theta):
     r = rng(6)
