@@ -32,7 +32,7 @@
 // Per 64-key tile a wave issues 16 MFMAs (512 cycles) and ~33 quarter-rate
 // v_exp_f32 (~530 cycles) plus the rest of the softmax, so the exponentials
 // alone bound it near 50% MFMA utilisation at head_dim 64; the running max is
-// therefore only moved, and O rescaled, when it grows by more than 2^8 in p
+// therefore only moved, and O rescaled, when it grows by more than 2^11 in p
 // (a wave-uniform branch), which removes most of the 32 rescale multiplies
 // per tile.
 #include <hip/hip_runtime.h>
