@@ -79,11 +79,16 @@ __global__ __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(4))) void 
     {
         const bool ok = qi < tile.nq;
         const bf16_t* qp = a.q + (long)(tile.q_row + (ok ? qi : 0)) * a.ldq + head * 64 + g * 8;
+        u32x4 r[4];
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            u32x4 r = ok ? *(const u32x4*)(qp + ks * 16) : u32x4{0, 0, 0, 0};
-            qf[ks] = __builtin_bit_cast(bf16x8, r);
-        }
+        for (int ks = 0; ks < 4; ++ks) r[ks] = ok ? *(const u32x4*)(qp + ks * 16) : u32x4{0, 0, 0, 0};
+        // Consume the loaded registers here, so the compiler waits for these
+        // loads once, before the key loop.  Otherwise its wait for them sits
+        // in front of every tile's first MFMA as vmcnt(0), which also waits
+        // out the next tile's K/V DMA issued just before it.
+        asm volatile("" : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]));
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) qf[ks] = __builtin_bit_cast(bf16x8, r[ks]);
     }
     const int qpos = tile.q_pos + qi;
 
@@ -169,13 +174,15 @@ __global__ __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(4))) void 
             }
         };
         // P = exp2(c·s - c·m) rounded to bf16, packed in pairs: pp[kb*8 + w]
-        // holds elements 2w, 2w+1 of block kb.  The row sum is taken over the
-        // same bf16 values (v_dot2 with (1, 1)), so numerator and denominator
-        // of the softmax see identical weights.
+        // holds elements 2w, 2w+1 of block kb.  The row sum adds the FP32
+        // values in four independent chains.  (v_dot2c_f32_bf16 over the packed
+        // pairs would need half the instructions, but on gfx950 it does not
+        // issue while an MFMA runs on the SIMD: measured ~7 cycles of MFMA
+        // time lost per dot2c, against none for v_add_f32.)
         uint32_t pp[16];
         float ls = 0.0f;
         auto exps = [&](const f32x16(&s)[2], float mc) {
-            ls = 0.0f;
+            float part[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -183,9 +190,9 @@ __global__ __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(4))) void 
                     const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][2 * w], c, -mc));
                     const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][2 * w + 1], c, -mc));
                     pp[kb * 8 + w] = pack2(p0, p1);
-                    ls = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pp[kb * 8 + w]),
-                                                         __builtin_bit_cast(bf16x2, 0x3f803f80u), ls, false);
+                    part[w & 3] += p0 + p1;
                 }
+            ls = (part[0] + part[1]) + (part[2] + part[3]);
         };
         // Masking is only needed where this wave's (query, key) block can hold
         // an invalid pair (decided per wave, so the branch is uniform): the
