@@ -509,6 +509,201 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     }
 }
 
+// Eight-wave variant for wide outputs (N >= 1024): one workgroup per CU owns
+// a 256-feature x BT-token tile (BT = 192 or 256), eight waves of 64
+// features x BT/2 tokens.  The operand DMA of a K step is 1 KB per
+// instruction through the texture addresser (TA), which drains one
+// instruction per ~16 cycles per CU; a wave blocks while its instructions
+// wait there.  When all waves issue their share right after the step's
+// barrier, every wave stalls for most of the burst before its first MFMA
+// (measured ~600-700 cycles per step).  Here waves 0-3 (one per SIMD) issue
+// all of a step's DMA, and waves 4-7, which share those SIMDs, start their
+// MFMAs at once; waves 0-3 compute after their burst, while 4-7 wait at the
+// next barrier.  The tile moves half the operand bytes per MFMA of a
+// 128x128 tile.  Each wave stages its epilogue through 8 KB of the last
+// step's buffers (plus a slack block when those are smaller than 64 KB).
+// Same products in the same K order as gemm_kernel: results are identical.
+template <int EPI, int BT>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void gemm_big_kernel(GemmArgs a) {
+    constexpr int BF = 256, FB = 2, TB = BT / 64;
+    constexpr int NW = BF / 32, NX = BT / 32;          // DMA instructions per loader wave and stage (W, X)
+    constexpr int WSTAGE = BF * BK, XSTAGE = BT * BK;  // bf16 elements per stage
+    constexpr int STG = 4096;                           // bf16 elements (8 KB) of staging per wave
+    constexpr int SLACK = 8 * STG > WSTAGE + XSTAGE ? 8 * STG - (WSTAGE + XSTAGE) : 0;
+    __shared__ __align__(1024) bf16_t smem[2 * WSTAGE + 2 * XSTAGE + SLACK];
+    bf16_t* const sW = smem;
+    bf16_t* const sX = smem + 2 * WSTAGE;
+    bf16_t* const sSlack = smem + 2 * WSTAGE + 2 * XSTAGE;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const bool loader = wave < 4;
+    const int nF = (a.n + BF - 1) / BF, nTk = (a.rows + BT - 1) / BT, ntiles = nF * nTk;
+    auto coords = [&](int b, int& f0, int& t0) {
+        const int xcd = b & 7, local = b >> 3, q8 = ntiles >> 3, r8 = ntiles & 7;
+        const int tile = xcd * q8 + (xcd < r8 ? xcd : r8) + local;
+        constexpr int GROUP = 4;
+        const int grp = tile / (GROUP * nF), gi = tile - grp * GROUP * nF;
+        const int gh = min(GROUP, nTk - grp * GROUP);
+        f0 = (gi / gh) * BF;
+        t0 = (grp * GROUP + gi % gh) * BT;
+    };
+    // Loader wave w's instruction j fills operand rows 32j + 8w .. +7 (lane i:
+    // row 32j + 8w + i/8, swizzled chunk); rows past the end of W or X fall
+    // outside the buffer resource's range, read as zeros, and land in
+    // accumulator rows that are never stored.
+    const int lrow = (wave & 3) * 8 + lane / 8;  // row within each 32-row block
+    const uint32_t lchunk = (uint32_t)(((lane & 7) ^ swz(lrow)) * 16);
+    struct Src {
+        i32x4 rw, rx;
+    };
+    auto setup = [&](int f0, int t0, Src& s) {
+        s.rw = make_rsrc(a.w + (long)f0 * a.k, (uint64_t)(a.n - f0) * a.k * 2);
+        s.rx = make_rsrc(a.x + (long)t0 * a.ldx, (uint64_t)(a.rows - 1 - t0) * a.ldx * 2 + (uint64_t)a.k * 2);
+    };
+    const uint32_t woff = (uint32_t)lrow * a.k * 2 + lchunk, xoff = (uint32_t)(lrow * a.ldx) * 2 + lchunk;
+    const uint32_t wstep = 32u * a.k * 2, xstep = 32u * (uint32_t)a.ldx * 2;  // bytes per 32 rows
+    const uint32_t wl0 = (uint32_t)(uintptr_t)&sW[(wave & 3) * 8 * 64];
+    const uint32_t xl0 = (uint32_t)(uintptr_t)&sX[(wave & 3) * 8 * 64];
+    auto issue = [&](const Src& s, int kt, int st) {
+        const uint32_t kb = (uint32_t)kt * BK * 2;
+#pragma unroll
+        for (int j = 0; j < (NW > NX ? NW : NX); ++j) {
+            if (j < NW) {
+                const uint32_t lw = __builtin_amdgcn_readfirstlane(wl0 + (st * WSTAGE + j * 32 * 64) * 2);
+                asm volatile("buffer_load_dwordx4 %1, %2, %3 offen lds" ::"{m0}"(lw), "v"(woff + j * wstep),
+                             "s"(s.rw), "s"(kb)
+                             : "memory");
+            }
+            if (j < NX) {
+                const uint32_t lx = __builtin_amdgcn_readfirstlane(xl0 + (st * XSTAGE + j * 32 * 64) * 2);
+                asm volatile("buffer_load_dwordx4 %1, %2, %3 offen lds" ::"{m0}"(lx), "v"(xoff + j * xstep),
+                             "s"(s.rx), "s"(kb)
+                             : "memory");
+            }
+        }
+    };
+    const int wf = wave & 3, wt = wave >> 2, lr = lane & 31, lg = lane >> 5;
+    const int G = gridDim.x, KT = a.k / BK;
+    int cur = blockIdx.x, f0, t0, base = 0;
+    if (cur >= ntiles) return;
+    coords(cur, f0, t0);
+    Src sc;
+    setup(f0, t0, sc);
+    if (loader) issue(sc, 0, 0);
+    bool first = true;
+    while (true) {
+        const int nxt = cur + G;
+        const bool has_next = nxt < ntiles;
+        int nf0 = 0, nt0 = 0;
+        Src sn = sc;
+        if (has_next) {
+            coords(nxt, nf0, nt0);
+            setup(nf0, nt0, sn);
+        }
+        // RoPE: this lane's token positions are loaded at the tile's start and
+        // the first 32-token block's cos/sin values during the last K step,
+        // so the epilogue, which every wave of the CU runs at once, does not
+        // start by waiting on two dependent loads (later blocks wait on one).
+        // (256-token tiles keep the loads inside the epilogue: with the
+        // prefetch their registers do not fit two waves per SIMD.)
+        constexpr bool ROPE = EPI == JH_EPI_ROPE_BF16 && TB <= 3;
+        const bool rot = ROPE && f0 + wf * 64 < a.rope_cols;
+        int rp[ROPE ? TB : 1];
+        if constexpr (ROPE) {
+#pragma unroll
+            for (int j = 0; j < TB; ++j)
+                rp[j] = rot ? (a.pos[min(t0 + wt * (BT / 2) + j * 32 + lr, a.rows - 1)] & 0xffff) * 32 : 0;
+        }
+        f32x4 rc[4], rs[4];
+        auto rope_load = [&](int j) {
+            if constexpr (ROPE) {
+                if (rot) {
+#pragma unroll
+                    for (int qd = 0; qd < 4; ++qd) {
+                        rc[qd] = *(const f32x4*)(a.cos_t + rp[j] + qd * 8 + lg * 4);
+                        rs[qd] = *(const f32x4*)(a.sin_t + rp[j] + qd * 8 + lg * 4);
+                    }
+                }
+            }
+        };
+        f32x16 acc[FB][TB];
+#pragma unroll
+        for (int i = 0; i < FB; ++i)
+#pragma unroll
+            for (int j = 0; j < TB; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+        for (int kt = 0; kt < KT; ++kt) {
+            const int st = (base + kt) & 1;
+            if (kt > 0 || first) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+            if (kt + 1 == KT) rope_load(0);
+            if (loader) {
+                if (kt + 1 < KT) issue(sc, kt + 1, st ^ 1);
+                else if (has_next) issue(sn, 0, st ^ 1);
+            }
+            const bf16_t* W = sW + st * WSTAGE;
+            const bf16_t* X = sX + st * XSTAGE;
+            bf16x8 af[2][FB], bx[2][TB];
+            auto load = [&](int ks, int s) {
+                const int c = ks * 2 + lg;
+#pragma unroll
+                for (int i = 0; i < FB; ++i) {
+                    const int r = wf * 64 + i * 32 + lr;
+                    af[s][i] = *(const bf16x8*)&W[r * BK + ((c ^ swz(r)) * 8)];
+                }
+#pragma unroll
+                for (int j = 0; j < TB; ++j) {
+                    const int r = wt * (BT / 2) + j * 32 + lr;
+                    bx[s][j] = *(const bf16x8*)&X[r * BK + ((c ^ swz(r)) * 8)];
+                }
+            };
+            load(0, 0);
+            load(1, 1);
+#pragma unroll
+            for (int ks = 0; ks < BK / 16; ++ks) {
+                const int s = ks & 1;
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int i = 0; i < FB; ++i)
+#pragma unroll
+                    for (int j = 0; j < TB; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[s][i], bx[s][j], acc[i][j], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+                if (ks + 2 < BK / 16) load(ks + 2, s);
+            }
+        }
+        const int st_last = (base + KT - 1) & 1;
+        __syncthreads();  // every wave is done reading the last step's buffers
+        if (has_next) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        // 8 KB of staging per wave: the last step's W buffer, then its X
+        // buffer, then the slack block.
+        const int so = wave * STG;
+        bf16_t* const sbase = so < WSTAGE ? sW + st_last * WSTAGE + so
+                              : so < WSTAGE + XSTAGE ? sX + st_last * XSTAGE + (so - WSTAGE)
+                                                     : sSlack + (so - WSTAGE - XSTAGE);
+        float* const stg = (float*)sbase;
+        if (f0 + wf * 64 < a.n) {
+#pragma unroll
+            for (int j = 0; j < TB; ++j) {
+                f32x16 part[2][1] = {{acc[0][j]}, {acc[1][j]}};
+                if constexpr (ROPE) {
+                    if (j > 0) rope_load(j);
+                    epilogue<EPI, 1>(a, part, f0 + wf * 64, t0 + wt * (BT / 2) + j * 32, lane, stg, rc, rs);
+                } else {
+                    epilogue<EPI, 1>(a, part, f0 + wf * 64, t0 + wt * (BT / 2) + j * 32, lane, stg);
+                }
+            }
+        }
+        if (!has_next) break;
+        cur = nxt;
+        f0 = nf0;
+        t0 = nt0;
+        sc = sn;
+        base = (base + KT) & 1;
+        first = false;
+    }
+}
+
 // Small batches in one launch, without the split-K workspace or its reduce
 // kernel.  A workgroup owns a 64-feature x 32-token tile and the whole K: every
 // operand chunk reaches LDS in a single round of DMA, laid out as K/64 blocks
@@ -776,19 +971,47 @@ void launch_cfg(const GemmArgs& a, hipStream_t s) {
         return;
     }
     const int resident = resident_tiles();
-    if (a.gather) JH_LAUNCH((gemm_kernel<EPI, true>), dim3(blocks), dim3(256), 0, s, a);
-    else if (blocks > resident) {
-        // 128x192 tiles when their rounds of resident workgroups, at 1.5x the
-        // work each, cost no more than the 128x128 tiles' (config1's 9482
-        // tokens: 2 rounds against 3); otherwise the finer tiles quantise better.
+    if (a.gather) {
+        JH_LAUNCH((gemm_kernel<EPI, true>), dim3(blocks), dim3(256), 0, s, a);
+    } else if (blocks > resident) {
+        // More tiles than resident workgroups.  Each candidate is costed as its
+        // rounds of resident workgroups times the time one round took on
+        // MI355X (K = 768, N = 2304, one box): persistent 128x128 12.9 us and
+        // 128x192 20.6 us at two workgroups per CU; eight-wave 256x192 19.0
+        // and 256x256 22.4 us at one per CU.
+        auto rounds = [](long tiles, long slots) { return (tiles + slots - 1) / slots; };
         const long t192 = (long)((a.n + 127) / 128) * ((a.rows + 191) / 192);
-        const long r128 = (blocks + resident - 1) / resident, r192 = (t192 + resident - 1) / resident;
-        if (t192 >= resident && 3 * r192 <= 2 * r128)
+        const long r128 = rounds(blocks, resident), r192 = rounds(t192, resident);
+        // Persistent 128-feature tiles: 192 tokens when their rounds, at 1.5x
+        // the work each, cost no more than the 128-token tiles' rounds.
+        const bool p192 = t192 >= resident && 3 * r192 <= 2 * r128;
+        double best = p192 ? r192 * 20.6 : r128 * 12.9;
+        int big = 0;
+        if (a.n >= 1024) {
+            const int grid = resident / 2;
+            const long nF = (a.n + 255) / 256;
+            // (256x128 never beats the persistent 128x128 tiles: it has at least
+            // their rounds at a higher cost per round.)
+            const int bts[2] = {256, 192};
+            const double per_round[2] = {22.4, 19.0};
+            for (int c = 0; c < 2; ++c) {
+                const double cost = rounds(nF * ((a.rows + bts[c] - 1) / bts[c]), grid) * per_round[c];
+                if (cost < best) best = cost, big = bts[c];
+            }
+        }
+        if (big) {
+            const long tiles = (long)((a.n + 255) / 256) * ((a.rows + big - 1) / big);
+            const dim3 g((unsigned)std::min<long>(resident / 2, tiles));
+            if (big == 256) JH_LAUNCH((gemm_big_kernel<EPI, 256>), g, dim3(512), 0, s, a);
+            else JH_LAUNCH((gemm_big_kernel<EPI, 192>), g, dim3(512), 0, s, a);
+        } else if (p192) {
             JH_LAUNCH((gemm_persist_kernel<EPI, 192>), dim3(resident), dim3(256), 0, s, a);
-        else
+        } else {
             JH_LAUNCH((gemm_persist_kernel<EPI>), dim3(resident), dim3(256), 0, s, a);
+        }
+    } else {
+        JH_LAUNCH((gemm_kernel<EPI, false>), dim3(blocks), dim3(256), 0, s, a);
     }
-    else JH_LAUNCH((gemm_kernel<EPI, false>), dim3(blocks), dim3(256), 0, s, a);
     HIP_CHECK(hipGetLastError());
 }
 

@@ -137,14 +137,10 @@ def test_gemm_sweep_shapes_full_size(n, k, epi):
     assert bool((d <= 4e-3 * expect.abs() + 1e-5).all()), d.max().item()
 
 
-@pytest.mark.parametrize("rows,n,k,epi", [(9482, 2304, 768, abi.EPI_STORE_BF16), (9482, 2304, 768, abi.EPI_GEGLU_BF16),
-                                          (9482, 2304, 768, abi.EPI_ROPE_BF16), (9482, 2304, 768, abi.EPI_BIAS_BF16),
-                                          (24000, 768, 768, abi.EPI_RESID_F32)])
-def test_gemm_192_token_tiles(rows, n, k, epi):
-    """Shapes whose persistent GEMM runs 128-feature x 192-token tiles (config1's 9482 tokens: 2 rounds of
-    resident workgroups against 3 for 128x128 tiles; 24000 x 768: 2 against 3), every epilogue family, against a
-    torch FP32 product of the same bf16 operands on the GPU."""
-    g = torch.Generator(device="cuda").manual_seed(rows + n + epi)
+def _check_wide_gemm(rows, n, k, epi, seed):
+    """One GEMM of random bf16 operands through the C-ABI against a torch FP32 product of the same operands on the
+    GPU, with the epilogue applied in FP32 (bf16 outputs within 4e-3 relative, FP32 residual within 1e-4)."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
     x = torch.randn(rows, k, device="cuda", generator=g).to(BF16)
     w = (torch.randn(n, k, device="cuda", generator=g) * 0.02).to(BF16)
     prod = x.float() @ w.float().T
@@ -160,9 +156,11 @@ def test_gemm_192_token_tiles(rows, n, k, epi):
         inter = n // 2
         expect = torch.nn.functional.gelu(prod[:, :inter]) * prod[:, inter:]
         wk = dev(hip.interleave_geglu(w.float().cpu().numpy()), BF16)
-    elif epi == abi.EPI_BIAS_BF16:
+    elif epi in (abi.EPI_BIAS_BF16, abi.EPI_BIAS_RELU_BF16):
         bias = torch.randn(n, device="cuda", generator=g) * 0.1
         expect = prod + bias
+        if epi == abi.EPI_BIAS_RELU_BF16:
+            expect = expect.clamp_min(0.0)
         kw = dict(bias=bias)
     elif epi == abi.EPI_ROPE_BF16:
         rc = 2 * n // 3  # q and k rotated, v not
@@ -187,6 +185,29 @@ def test_gemm_192_token_tiles(rows, n, k, epi):
     d = (out.float() - expect).abs()
     ref = scale if scale is not None else expect.abs()
     assert bool((d <= 4e-3 * ref + 1e-5).all()), d.max().item()
+
+
+@pytest.mark.parametrize("rows,n,k,epi", [(24000, 768, 768, abi.EPI_STORE_BF16), (24000, 768, 768, abi.EPI_ROPE_BF16),
+                                          (24000, 768, 768, abi.EPI_GEGLU_BF16), (24000, 768, 768, abi.EPI_BIAS_BF16),
+                                          (24000, 768, 768, abi.EPI_RESID_F32)])
+def test_gemm_192_token_tiles(rows, n, k, epi):
+    """Shapes whose persistent GEMM runs 128-feature x 192-token tiles (24000 x 768: 750 tiles, 2 rounds of the
+    512 resident workgroups against 3 for 128x128 tiles; N < 1024 never takes the eight-wave kernel), every
+    epilogue family, against torch FP32."""
+    _check_wide_gemm(rows, n, k, epi, rows + n + epi)
+
+
+@pytest.mark.parametrize("rows,n,k,epi", [(9482, 2304, 768, abi.EPI_STORE_BF16), (9482, 2304, 768, abi.EPI_GEGLU_BF16),
+                                          (9482, 2304, 768, abi.EPI_ROPE_BF16), (9482, 2304, 768, abi.EPI_BIAS_BF16),
+                                          (7556, 1152, 384, abi.EPI_ROPE_BF16), (7556, 2304, 384, abi.EPI_GEGLU_BF16),
+                                          (16500, 1152, 384, abi.EPI_BIAS_RELU_BF16),
+                                          (32768, 2304, 768, abi.EPI_STORE_BF16), (32768, 2304, 768, abi.EPI_GEGLU_BF16)])
+def test_gemm_eight_wave_tiles(rows, n, k, epi):
+    """Shapes routed to the eight-wave 256-feature GEMM: 256x192 tiles at config1's 9482 tokens, at the Julia-1
+    widths (N = 1152 leaves half a 256-feature tile, whose rows past N read as zeros from the buffer range check)
+    and with token tiles cut at the end, and 256x256 tiles at 32768 tokens; every epilogue family except the FP32
+    residual (N = 768 stays on the four-wave kernels), against torch FP32."""
+    _check_wide_gemm(rows, n, k, epi, rows + 3 * n + epi)
 
 
 @pytest.mark.parametrize("theta", [10000.0, 160000.0])
