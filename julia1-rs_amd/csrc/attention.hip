@@ -100,23 +100,31 @@ __global__ __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(4))) void 
 
     // DMA of one K/V tile into buffer `buf`: wave w fills rows [16w, 16w+16)
     // of both with two 1 KB instructions each; lane i of instruction j takes
-    // row 16w + 8j + i/8, physical slot i%8.  Rows past the sequence end are
-    // clamped onto its last key (masked to -inf before the softmax; their
-    // finite V rows then contribute exactly 0).
+    // row 16w + 8j + i/8, physical slot i%8.  The lane's byte offsets are
+    // fixed per row (the tile adds k0 rows); rows past the sequence end fall
+    // outside the buffer resource's range and read as zeros (they are masked
+    // to -inf before the softmax, and their zero V rows contribute nothing).
     const i32x4 rsk = make_rsrc(kbase, ((uint64_t)(tile.kv_len - 1) * a.ldkv + 64) * 2);
     const i32x4 rsv = make_rsrc(vbase, ((uint64_t)(tile.kv_len - 1) * a.ldkv + 64) * 2);
     const uint32_t lk0 = (uint32_t)(uintptr_t)&sK[0][0], lv0 = (uint32_t)(uintptr_t)&sV[0][0];
+    uint32_t okb[2], ovb[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int row = 16 * wave + 8 * j + (lane >> 3);
+        okb[j] = (uint32_t)(row * a.ldkv + (((lane & 7) ^ kswz(row)) * 8)) * 2;
+        ovb[j] = (uint32_t)(row * a.ldkv + (((lane & 7) ^ vswz(row)) * 8)) * 2;
+    }
     auto issue = [&](int k0, int buf) {
+        const uint32_t kt = (uint32_t)(k0 * a.ldkv) * 2;  // bytes of the tile's first key row
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-            const int r0 = 16 * wave + 8 * j, row = r0 + (lane >> 3);
-            const int key = min(k0 + row, kend - 1);
+            const int r0 = 16 * wave + 8 * j;
             const uint32_t lk = __builtin_amdgcn_readfirstlane(lk0 + (buf * KT * 64 + r0 * 64) * 2);
             const uint32_t lv = __builtin_amdgcn_readfirstlane(lv0 + (buf * KT * 64 + r0 * 64) * 2);
-            const uint32_t ok = (uint32_t)(key * a.ldkv + (((lane & 7) ^ kswz(row)) * 8)) * 2;
-            const uint32_t ov = (uint32_t)(key * a.ldkv + (((lane & 7) ^ vswz(row)) * 8)) * 2;
-            asm volatile("buffer_load_dwordx4 %1, %2, 0 offen lds" ::"{m0}"(lk), "v"(ok), "s"(rsk) : "memory");
-            asm volatile("buffer_load_dwordx4 %1, %2, 0 offen lds" ::"{m0}"(lv), "v"(ov), "s"(rsv) : "memory");
+            asm volatile("buffer_load_dwordx4 %1, %2, 0 offen lds" ::"{m0}"(lk), "v"(okb[j] + kt), "s"(rsk)
+                         : "memory");
+            asm volatile("buffer_load_dwordx4 %1, %2, 0 offen lds" ::"{m0}"(lv), "v"(ovb[j] + kt), "s"(rsv)
+                         : "memory");
         }
     };
     // Transposing V reads: this lane's 16-lane group G and index j select
