@@ -405,6 +405,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     const int wf = wave & 1, wt = wave >> 1, lr = lane & 31, lg = lane >> 5;
     const int G = gridDim.x, KT = a.k / BK;
     int cur = blockIdx.x, f0, t0, base = 0;
+    // A grid larger than the tile count (launch_cfg never makes one) would
+    // otherwise compute tile coordinates past the matrix for the extra
+    // workgroups and aim their DMA outside the operands.
+    if (cur >= ntiles) return;
     coords(cur, f0, t0);
     Src sc;
     setup(f0, t0, sc);
