@@ -29,12 +29,12 @@
 // Sliding-window tiles only visit keys in [q_pos - window, q_pos + nq - 1 +
 // window] ∩ [0, kv_len), with per-element masking of |q - k| <= window.
 //
-// Per 64-key tile a wave issues 16 MFMAs (512 cycles) and ~33 quarter-rate
-// v_exp_f32 (~530 cycles) plus the rest of the softmax, so the exponentials
-// alone bound it near 50% MFMA utilisation at head_dim 64; the running max is
-// therefore only moved, and O rescaled, when it grows by more than 2^11 in p
-// (a wave-uniform branch), which removes most of the 32 rescale multiplies
-// per tile.
+// Per 64-key tile a wave issues 16 MFMAs (512 cycles of its SIMD's MFMA pipe)
+// against ~150 other VALU instructions, 32 of them v_exp_f32 (~8 cycles each
+// on gfx950, the others 2-5); measured, MFMA and VALU time largely add up at
+// head_dim 64, so the softmax is kept lean: the running max is only moved,
+// and O rescaled, when it grows by more than 2^11 in p (a wave-uniform
+// branch), which removes most of the 32 rescale multiplies per tile.
 #include <hip/hip_runtime.h>
 
 #include "kernels.hpp"
