@@ -83,6 +83,22 @@ int jh_op_gemm_splitk_noalloc(int epilogue, const void* x, size_t ldx, const int
                               size_t col, const float* bias, const int32_t* pos, const float* cos_t,
                               const float* sin_t, size_t rope_cols, int splits, void* stream);
 
+/*
+ * jh_op_gemm whose X operand is bf16(LayerNorm(xf[r]; ln_w, ln_b, eps)), the
+ * normalisation computed in the small-batch kernel's prologue exactly as
+ * jh_op_layer_norm computes it (the same bits).  xf f32 [rows, k] with row
+ * stride ldx floats (ldx % 4 == 0, 16-byte aligned); ln_w f32 [k], ln_b f32 [k]
+ * or NULL.  k = hidden in {128, 256, 384, 512, 768}; epilogues STORE_BF16,
+ * ROPE_BF16 and GEGLU_BF16; one workgroup per 64 x 32 output tile, so it is
+ * meant for the few-token batches the backend runs on the small-batch kernel.
+ * Replaces ln_bf16 (src/cuda/kernels.cu:97-109) followed by cuBLAS gemm_ex
+ * (src/cuda/mod.rs:347-375) for those batches.
+ */
+int jh_op_gemm_ln(int epilogue, const float* xf, size_t ldx, size_t rows, const void* w, size_t n,
+                  size_t k, void* out, size_t ldo, size_t col, const int32_t* pos, const float* cos_t,
+                  const float* sin_t, size_t rope_cols, const float* ln_w, const float* ln_b, float eps,
+                  void* stream);
+
 /* Reorder a host FP32 Wi [2*inter, k] into the gate/up interleave JH_EPI_GEGLU_BF16 expects. */
 void jh_op_interleave_geglu(const float* wi, size_t inter, size_t k, float* out);
 

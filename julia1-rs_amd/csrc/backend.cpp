@@ -428,6 +428,44 @@ struct jh_model {
         });
     }
 
+    // GEMM whose X operand is bf16(LN(xf row)) with weights ln_w, computed in
+    // the small-batch kernel's prologue (K = hidden).
+    void gemm_ln(int cls, int epi, const float* xf, size_t rows, const float* ln_w, const bf16_t* w, int n, void* out,
+                 long ldo, const float* cos_t = nullptr, const float* sin_t = nullptr, int rope_cols = 0) {
+        const int k = h;
+        GemmArgs a{nullptr, (long)k, nullptr, (int)rows, w, n, k, out, ldo, 0, nullptr,
+                   (const int32_t*)d_tok, cos_t, sin_t, rope_cols};
+        a.xf = xf;
+        a.ln_w = ln_w;
+        a.ln_eps = eps;
+        timed(cls, 2.0 * rows * n * k, gemm_bytes(epi, rows, n, k) + 2.0 * rows * k,
+              [&] { launch_gemm(epi, a, stream); });
+        if (profiling && !replay[cls]) replay[cls] = [epi, a, st = stream] { launch_gemm(epi, a, st); };
+    }
+
+    // Whether every encoder GEMM of the staged batch runs as one launch of the
+    // small-batch kernel (split-K mode, few tokens).  Then the residual GEMMs
+    // add straight into x and the LayerNorms before Wqkv and Wi run in those
+    // GEMMs' prologues: five launches per layer instead of seven (a split-K
+    // partial pass and a reduce + LayerNorm kernel per residual GEMM).
+    bool fused_small_layers() {
+        if (!use_splitk || T == 0 || nlayers == 0) return false;
+        if (h != 128 && h != 256 && h != 384 && h != 512 && h != 768) return false;
+        const EncLayer& L = layers[0];
+        auto small = [&](int epi, const void* xp, long ldx, const bf16_t* w, int n, int k, void* out, long ldo) {
+            GemmArgs a{(const bf16_t*)xp, ldx, nullptr, (int)T, w, n, k, out, ldo, 0, nullptr, nullptr, nullptr,
+                       nullptr, 0};
+            a.partial = splitk.as<float>();
+            a.partial_bytes = kSplitkBytes;
+            return gemm_uses_small(epi, a);
+        };
+        const int H = h;
+        return small(JH_EPI_ROPE_BF16, xn.p, H, L.wqkv.as<bf16_t>(), 3 * H, H, qkv.p, 3 * H) &&
+               small(JH_EPI_RESID_F32, ctx.p, H, L.wo.as<bf16_t>(), H, H, x.p, H) &&
+               small(JH_EPI_GEGLU_BF16, xn.p, H, L.wi.as<bf16_t>(), 2 * inter, H, hbuf.p, inter) &&
+               small(JH_EPI_RESID_F32, hbuf.p, inter, L.wo2.as<bf16_t>(), H, inter, x.p, H);
+    }
+
     void attention(int cls, const bf16_t* q, long ldq, const bf16_t* k, const bf16_t* v, long ldkv, bf16_t* out,
                    long ldo, const AttnTile* tiles, size_t n, int nheads, int window, double pairs, double qrows) {
         AttnArgs a{q, ldq, k, v, ldkv, out, ldo, tiles, (int)n, nheads, window, 0.125f * 1.4426950408889634f};
@@ -449,8 +487,32 @@ struct jh_model {
                             xn.as<bf16_t>(), stream);
         });
         bool xn_ready = false;  // xn already holds this layer's attn_norm(x) (fused into the previous Wo2)
+        const bool fused = fused_small_layers();
         for (int l = 0; l < upto; ++l) {
             EncLayer& L = layers[l];
+            if (fused) {
+                const float* cos_t = ropes[L.rope].first.as<float>();
+                const float* sin_t = ropes[L.rope].second.as<float>();
+                if (L.attn_norm.p)
+                    gemm_ln(K_QKV, JH_EPI_ROPE_BF16, x.as<float>(), t, L.attn_norm.as<float>(), L.wqkv.as<bf16_t>(),
+                            3 * H, qkv.p, 3 * H, cos_t, sin_t, 2 * H);
+                else
+                    gemm(K_QKV, JH_EPI_ROPE_BF16, xn.p, H, nullptr, t, L.wqkv.as<bf16_t>(), 3 * H, H, qkv.p, 3 * H, 0,
+                         nullptr, cos_t, sin_t, 2 * H);
+                const bf16_t* q = qkv.as<bf16_t>();
+                if (L.global)
+                    attention(K_ATTN_GLOBAL, q, 3 * H, q + H, q + 2 * H, 3 * H, ctx.as<bf16_t>(), H, d_tiles, ntiles,
+                              heads, -1, pairs_global, (double)t);
+                else
+                    attention(K_ATTN_LOCAL, q, 3 * H, q + H, q + 2 * H, 3 * H, ctx.as<bf16_t>(), H, d_tiles, ntiles,
+                              heads, half_window, pairs_local, (double)t);
+                gemm(K_WO, JH_EPI_RESID_F32, ctx.p, H, nullptr, t, L.wo.as<bf16_t>(), H, H, x.p, H, 0, nullptr);
+                gemm_ln(K_WI, JH_EPI_GEGLU_BF16, x.as<float>(), t, L.mlp_norm.as<float>(), L.wi.as<bf16_t>(),
+                        2 * inter, hbuf.p, inter);
+                gemm(K_WO2, JH_EPI_RESID_F32, hbuf.p, inter, nullptr, t, L.wo2.as<bf16_t>(), H, inter, x.p, H, 0,
+                     nullptr);
+                continue;
+            }
             if (L.attn_norm.p && !xn_ready)
                 layer_norm(K_LN, x.as<float>(), t, L.attn_norm.as<float>(), nullptr, eps, xn.as<bf16_t>());
             xn_ready = false;

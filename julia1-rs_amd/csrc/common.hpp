@@ -68,6 +68,15 @@ __device__ inline float wave_sum(float v) {
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, JH_WAVE);
     return v;
 }
+// wave_sum of N values at once (the same steps for each), so their shuffles
+// share each LDS round trip.
+template <int N>
+__device__ inline void wave_sum_n(float (&v)[N]) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1)
+#pragma unroll
+        for (int r = 0; r < N; ++r) v[r] += __shfl_xor(v[r], o, JH_WAVE);
+}
 
 __device__ inline float wave_max(float v) {
 #pragma unroll

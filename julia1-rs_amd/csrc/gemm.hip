@@ -27,6 +27,7 @@
 
 #include "../../include/julia1_hip_ops.h"
 #include "kernels.hpp"
+#include "rowvec.hpp"
 
 namespace {
 
@@ -708,106 +709,250 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
     }
 }
 
-// Small batches in one launch, without the split-K workspace or its reduce
-// kernel.  A workgroup owns a 64-feature x 32-token tile and the whole K: every
-// operand chunk reaches LDS in a single round of DMA, laid out as K/64 blocks
-// of the main kernel's stage layout (so the fragment reads are the same
-// conflict-free ones).  The four waves each multiply a quarter of the 16-deep
-// K slices; waves 1-3 hand their partial tiles to wave 0 through LDS, which
-// adds them in wave order (deterministic) and runs the epilogue.  For a
-// ~160-token request this replaces a split-K pass plus a reduce kernel
-// (two dependent launches of ~5 and ~4 us) by one launch.
-constexpr int SMALL_KMAX = 768;  // (64 + 32) rows x 768 x 2 B = 144 KB of LDS
-constexpr int SMALL_BF = 64, SMALL_BT = 32;
+// Elementwise epilogue of FP32 sums for one output row t, features f .. f+3
+// (epilogues without a 64-feature pairing).
+template <int EPI>
+__device__ inline void finish_one(const GemmArgs& a, long t, int f, f32x4 v) {
+    const bool biased = EPI == JH_EPI_BIAS_BF16 || EPI == JH_EPI_BIAS_RELU_BF16 || EPI == JH_EPI_BIAS_F32 ||
+                        (EPI == JH_EPI_RESID_F32 && a.bias);
+    if (biased) {
+        const f32x4 bb = *(const f32x4*)(a.bias + f);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[e] += bb[e];
+            if constexpr (EPI == JH_EPI_BIAS_RELU_BF16) v[e] = fmaxf(v[e], 0.0f);
+        }
+    }
+    const long c = a.col + f;
+    if constexpr (EPI == JH_EPI_RESID_F32) {
+        float* o = (float*)a.out + t * a.ldo + c;
+        f32x4 r = *(const f32x4*)o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) r[e] += v[e];
+        *(f32x4*)o = r;
+    } else if constexpr (EPI == JH_EPI_BIAS_F32) {
+        *(f32x4*)((float*)a.out + t * a.ldo + c) = v;
+    } else {
+        *(u32x2*)((bf16_t*)a.out + t * a.ldo + c) = u32x2{pack2(v[0], v[1]), pack2(v[2], v[3])};
+    }
+}
 
-template <int EPI, bool GATHER>
+// The same for features slab + 4q .. +3 (lo) and slab + 32 + 4q .. +3 (hi) of
+// a 64-feature block: the RoPE pair (d, d+32) and the GEGLU pair (gate, up)
+// of an output are both here.
+template <int EPI>
+__device__ inline void finish_pair(const GemmArgs& a, long t, int slab, int q, f32x4 lo, f32x4 hi) {
+    auto store_bf16 = [&](long col, f32x4 v) {
+        *(u32x2*)((bf16_t*)a.out + t * a.ldo + col) = u32x2{pack2(v[0], v[1]), pack2(v[2], v[3])};
+    };
+    const long c0 = a.col + slab + 4 * q;
+    if constexpr (EPI == JH_EPI_ROPE_BF16) {
+        if (slab < a.rope_cols) {
+            const long ps = (long)(a.pos[t] & 0xffff) * 32 + 4 * q;
+            const f32x4 c = *(const f32x4*)(a.cos_t + ps), sn = *(const f32x4*)(a.sin_t + ps);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float x0 = lo[e], x1 = hi[e];
+                lo[e] = x0 * c[e] - x1 * sn[e];
+                hi[e] = x1 * c[e] + x0 * sn[e];
+            }
+        }
+        store_bf16(c0, lo);
+        store_bf16(c0 + 32, hi);
+    } else if constexpr (EPI == JH_EPI_GEGLU_BF16) {
+        f32x4 g;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) g[e] = gelu_erf(lo[e]) * hi[e];
+        store_bf16(a.col + slab / 2 + 4 * q, g);
+    } else {
+        finish_one<EPI>(a, t, slab + 4 * q, lo);
+        finish_one<EPI>(a, t, slab + 32 + 4 * q, hi);
+    }
+}
+
+// Small batches in one launch, without the split-K workspace or its reduce
+// kernel.  A workgroup owns a BF-feature (64 or 32) x 32-token tile and the
+// whole K, resident in LDS as K/64 segments of the main kernel's stage layout
+// (so the fragment reads are the same conflict-free ones): 144 KB at most, so
+// K <= 768 for 64-feature tiles and K <= 1152 for 32-feature tiles.  Each
+// segment's DMA is split evenly over the four waves and issued SMALL_DEPTH
+// segments ahead; after a per-segment wait and barrier all four waves
+// multiply it, wave w the 16-deep slice 4g + w, so the MFMAs run while later
+// segments are still arriving (measured on MI355X at 128 tokens: the whole-K
+// fetch of a 64x32 tile takes ~3 us with the weights cold in L2, against
+// ~1.2 us of MFMA and LDS reads).  The four partial tiles are summed through
+// LDS in wave order (deterministic) by all four waves, 8 tokens each, which
+// then apply the epilogue.
+//
+// LayerNorm prologue (LN_EPL > 0, hidden = 64 * LN_EPL = K): X comes from
+// FP32 rows.  Each wave loads its 8 rows after the first W segments are
+// issued, normalises them as layer_norm_kernel does (same code, same bits)
+// and writes the bf16 rows into the X segments; the first segment's barrier
+// publishes them.  This replaces a LayerNorm launch between a residual GEMM
+// and the next GEMM.
+constexpr int SMALL_LDS = 96 * 768;  // bf16 elements of operand LDS per workgroup (144 KB)
+constexpr int SMALL_BT = 32;
+constexpr int SMALL_DEPTH = 6;  // K segments in flight ahead of the one being multiplied
+template <int BF>
+constexpr int small_kmax() {
+    return SMALL_LDS / (BF + SMALL_BT) / 64 * 64;
+}
+
+// s_waitcnt vmcnt(n * PW), n in [0, SMALL_DEPTH]: all but this wave's DMA of
+// its last n issued segments (PW instructions each) has landed.
+template <int PW>
+__device__ inline void wait_segments(int n) {
+    static_assert(SMALL_DEPTH == 6 && PW * SMALL_DEPTH <= 63, "vmcnt range");
+    switch (n) {
+        case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+        case 1: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(PW) : "memory"); break;
+        case 2: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * PW) : "memory"); break;
+        case 3: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * PW) : "memory"); break;
+        case 4: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * PW) : "memory"); break;
+        case 5: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(5 * PW) : "memory"); break;
+        default: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(6 * PW) : "memory"); break;
+    }
+}
+
+template <int EPI, bool GATHER, int BF, int LN_EPL>
 __global__ __launch_bounds__(256) void gemm_small_kernel(GemmArgs a) {
-    constexpr int BF = SMALL_BF, BT = SMALL_BT;
-    __shared__ __align__(1024) bf16_t smem[(BF + BT) * SMALL_KMAX];
+    constexpr int BT = SMALL_BT, FB = BF / 32, NCH = BF / 4;
+    constexpr bool LNX = LN_EPL > 0;
+    constexpr int WI = BF / 8, XI = LNX ? 0 : BT / 8;  // DMA instructions (8 rows x 128 B) per K segment
+    constexpr int PW = (WI + XI) / 4;                  // ... per wave
+    static_assert((WI + XI) % 4 == 0 && (BF == 64 || BF == 32), "tile shape");
+    static_assert(!LNX || (BF == 64 && !GATHER), "LayerNorm prologue: 64-feature tiles, contiguous rows");
+    __shared__ __align__(1024) bf16_t smem[SMALL_LDS];
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int nF = a.n / BF;
     const int f0 = (int)(blockIdx.x % nF) * BF, t0 = (int)(blockIdx.x / nF) * BT;
     const int nseg = a.k / 64;  // 128-byte row segments
-    bf16_t* const sW = smem;                     // segment g: rows [0, BF) at sW + g*BF*64
-    bf16_t* const sX = smem + nseg * BF * 64;    // segment g: rows [0, BT) at sX + g*BT*64
-
-    // DMA: per segment 8 instructions of 8 W rows and 4 of 8 X rows; wave w
-    // issues instructions w, w+4, ...  Rows past the end are clamped (never
-    // stored), as in gemm_kernel.
-    const bf16_t* wt0 = a.w + (long)f0 * a.k;
-    const bf16_t* xt0 = a.x + (long)t0 * a.ldx;
-    const i32x4 rw = make_rsrc(wt0, (uint64_t)(a.n - f0) * a.k * 2);
-    const i32x4 rx = make_rsrc(xt0, (uint64_t)(a.rows - 1 - t0) * a.ldx * 2 + (uint64_t)a.k * 2);
+    bf16_t* const sW = smem;                   // segment g: rows [0, BF) at sW + g*BF*64
+    bf16_t* const sX = smem + nseg * BF * 64;  // segment g: rows [0, BT) at sX + g*BT*64
+    const i32x4 rw = make_rsrc(a.w + (long)f0 * a.k, (uint64_t)BF * a.k * 2);
+    const i32x4 rx = LNX ? i32x4{0, 0, 0, 0}
+                         : make_rsrc(a.x + (long)t0 * a.ldx, (uint64_t)(a.rows - 1 - t0) * a.ldx * 2 + (uint64_t)a.k * 2);
     const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
-    for (int i = wave; i < 12 * nseg; i += 4) {
-        const int g = i / 12, j = i - g * 12;  // wave-uniform
-        const int row = (j < 8 ? j : j - 8) * 8 + (lane >> 3);
-        const int c = (lane & 7) ^ ((row >> 1) & 7);
+
+    // Segment g: instructions [0, WI) bring W rows 8j .. 8j+7, [WI, WI+XI) X
+    // rows; wave w issues instructions w*PW .. w*PW+PW-1.  Token rows past the
+    // end are clamped (their products are never stored).
+    auto issue = [&](int g) {
         const uint32_t kb = (uint32_t)g * 128;
-        if (j < 8) {
-            const uint32_t l = __builtin_amdgcn_readfirstlane(lds0 + (uint32_t)((g * BF + j * 8) * 64) * 2);
-            const uint32_t off = (uint32_t)((min(f0 + row, a.n - 1) - f0) * a.k + c * 8) * 2;
-            asm volatile("buffer_load_dwordx4 %1, %2, %3 offen lds" ::"{m0}"(l), "v"(off), "s"(rw), "s"(kb) : "memory");
-        } else {
-            const uint32_t l = __builtin_amdgcn_readfirstlane(
-                lds0 + (uint32_t)((nseg * BF * 64 + (g * BT + (j - 8) * 8) * 64) * 2));
-            const int t = min(t0 + row, a.rows - 1);
-            if constexpr (GATHER) {
-                const bf16_t* src = a.x + (long)a.gather[t] * a.ldx + g * 64 + c * 8;
-                asm volatile("global_load_lds_dwordx4 %1, off" ::"{m0}"(l), "v"(src) : "memory");
-            } else {
-                const uint32_t off = (uint32_t)((t - t0) * (long)a.ldx + c * 8) * 2;
-                asm volatile("buffer_load_dwordx4 %1, %2, %3 offen lds" ::"{m0}"(l), "v"(off), "s"(rx), "s"(kb)
+#pragma unroll
+        for (int u = 0; u < PW; ++u) {
+            const int j = wave * PW + u;  // wave-uniform
+            if (j < WI) {
+                const int row = j * 8 + (lane >> 3);
+                const uint32_t l = __builtin_amdgcn_readfirstlane(lds0 + (uint32_t)((g * BF + j * 8) * 64) * 2);
+                const uint32_t off = (uint32_t)(row * a.k + (((lane & 7) ^ swz(row)) * 8)) * 2;
+                asm volatile("buffer_load_dwordx4 %1, %2, %3 offen lds" ::"{m0}"(l), "v"(off), "s"(rw), "s"(kb)
                              : "memory");
+            } else if constexpr (XI > 0) {
+                const int row = (j - WI) * 8 + (lane >> 3), c = (lane & 7) ^ swz(row);
+                const uint32_t l = __builtin_amdgcn_readfirstlane(
+                    lds0 + (uint32_t)((nseg * BF * 64 + (g * BT + (j - WI) * 8) * 64) * 2));
+                const int t = min(t0 + row, a.rows - 1);
+                if constexpr (GATHER) {
+                    const bf16_t* src = a.x + (long)a.gather[t] * a.ldx + g * 64 + c * 8;
+                    asm volatile("global_load_lds_dwordx4 %1, off" ::"{m0}"(l), "v"(src) : "memory");
+                } else {
+                    const uint32_t off = (uint32_t)((t - t0) * (long)a.ldx + c * 8) * 2;
+                    asm volatile("buffer_load_dwordx4 %1, %2, %3 offen lds" ::"{m0}"(l), "v"(off), "s"(rx), "s"(kb)
+                                 : "memory");
+                }
+            }
+        }
+    };
+
+    int issued = min(SMALL_DEPTH, nseg);
+    for (int g = 0; g < issued; ++g) issue(g);
+    if constexpr (LNX) {
+        // Loads complete in issue order, so these rows arrive after the W
+        // segments issued above; the compiler's waits for them cover that.
+        constexpr int VEC = RowVec<LN_EPL>::VEC;
+        RowVec<LN_EPL> xr[8], lw, lb;
+#pragma unroll
+        for (int r = 0; r < 8; ++r) xr[r].load(a.xf + (long)min(t0 + wave * 8 + r, a.rows - 1) * a.ldx, lane);
+        lw.load(a.ln_w, lane);
+        if (a.ln_b) lb.load(a.ln_b, lane);
+        // RowVec::layer_norm's steps with the 8 rows' reductions interleaved.
+        float st[8], mean[8];
+#pragma unroll
+        for (int r = 0; r < 8; ++r) st[r] = xr[r].sum();
+        wave_sum_n(st);
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            mean[r] = st[r] * RowVec<LN_EPL>::kInvN;
+            st[r] = xr[r].sq_dev(mean[r]);
+        }
+        wave_sum_n(st);
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            const int rr = wave * 8 + r;
+            xr[r].scale_shift(mean[r], RowVec<LN_EPL>::rstd(st[r], a.ln_eps), lw, a.ln_b ? &lb : nullptr);
+#pragma unroll
+            for (int c = 0; c < RowVec<LN_EPL>::NC; ++c) {
+                const int kk = RowVec<LN_EPL>::index(c, lane), o = kk & 63;
+                bf16_t* d = sX + (kk >> 6) * BT * 64 + rr * 64 + (((o >> 3) ^ swz(rr)) * 8) + (o & 7);
+                const float* v = xr[r].v + c * VEC;
+                if constexpr (VEC == 4) *(u32x2*)d = u32x2{pack2(v[0], v[1]), pack2(v[2], v[3])};
+                else if constexpr (VEC == 2) *(uint32_t*)d = pack2(v[0], v[1]);
+                else *d = f2bf(v[0]);
             }
         }
     }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
 
-    // This wave's quarter of the K/16 slices: slice s lies in segment s/4 at
-    // chunk pair 2(s%4) + (lane >= 32).
-    const int lr = lane & 31, lg = lane >> 5;
-    f32x16 acc[2][1];
+    const int lr = lane & 31, lg = lane >> 5, c = wave * 2 + lg;  // chunk pair of slice 4g + wave
+    f32x16 acc[FB];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < FB; ++i)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) acc[i][0][e] = 0.0f;
-    const int nsl = a.k / 16, s0 = wave * (nsl / 4), s1 = s0 + nsl / 4;
-    for (int sl = s0; sl < s1; ++sl) {
-        const int g = sl >> 2, c = (sl & 3) * 2 + lg;
-        const bf16x8 bx = *(const bf16x8*)&sX[g * BT * 64 + lr * 64 + ((c ^ ((lr >> 1) & 7)) * 8)];
+        for (int e = 0; e < 16; ++e) acc[i][e] = 0.0f;
+    for (int g = 0; g < nseg; ++g) {
+        wait_segments<PW>(issued - g - 1);  // this wave's part of segment g has landed
+        __syncthreads();                     // ... and every wave's
+        if (issued < nseg) issue(issued++);
+        const bf16x8 bx = *(const bf16x8*)&sX[g * BT * 64 + lr * 64 + ((c ^ swz(lr)) * 8)];
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < FB; ++i) {
             const int r = i * 32 + lr;
-            const bf16x8 af = *(const bf16x8*)&sW[g * BF * 64 + r * 64 + ((c ^ ((r >> 1) & 7)) * 8)];
-            acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, bx, acc[i][0], 0, 0, 0);
+            const bf16x8 af = *(const bf16x8*)&sW[g * BF * 64 + r * 64 + ((c ^ swz(r)) * 8)];
+            acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, bx, acc[i], 0, 0, 0);
         }
     }
-    __syncthreads();  // operand LDS is free: reused for the partial tiles and the staging rows
-    // Partial tile of wave w (1..3): 8 blocks of 64 lanes x 16 B, element e of
-    // block q is acc[q/4][0][4(q%4) + e].
+    __syncthreads();  // operand LDS is free: reused for the partial tiles
+    // Partial tile of wave w: [token][NCH 16-byte chunks of 4 features], the
+    // chunk index XOR-swizzled by the token so both passes spread over banks.
+    // acc[i][4qd + e] is feature i*32 + qd*8 + 4*lg + e of token lr.
     float* const red = (float*)smem;
-    if (wave > 0) {
+    auto slot = [&](int w, int tok, int ch) { return ((w * BT + tok) * NCH + (ch ^ (tok & (NCH - 1)))) * 4; };
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
+    for (int i = 0; i < FB; ++i)
+#pragma unroll
+        for (int qd = 0; qd < 4; ++qd) {
             f32x4 v;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = acc[q >> 2][0][(q & 3) * 4 + e];
-            *(f32x4*)&red[(((wave - 1) * 8 + q) * 64 + lane) * 4] = v;
+            for (int e = 0; e < 4; ++e) v[e] = acc[i][qd * 4 + e];
+            *(f32x4*)&red[slot(wave, lr, i * 8 + qd * 2 + lg)] = v;
         }
-    }
     __syncthreads();
-    if (wave > 0) return;
+    // Wave w finishes tokens 8w .. 8w+7, lane -> (token 8w + lane/8, chunk q).
+    const int tl = wave * 8 + (lane >> 3), q = lane & 7;
+    const long t = t0 + tl;
+    if (t >= a.rows) return;
+    auto total = [&](int ch) {
+        f32x4 s = *(const f32x4*)&red[slot(0, tl, ch)];
 #pragma unroll
-    for (int w = 0; w < 3; ++w)
+        for (int w = 1; w < 4; ++w) {
+            const f32x4 v = *(const f32x4*)&red[slot(w, tl, ch)];
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            const f32x4 v = *(const f32x4*)&red[((w * 8 + q) * 64 + lane) * 4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) acc[q >> 2][0][(q & 3) * 4 + e] += v[e];
+            for (int e = 0; e < 4; ++e) s[e] += v[e];
         }
-    epilogue<EPI, 1>(a, acc, f0, t0, lane, red + 3 * 8 * 64 * 4);
+        return s;
+    };
+    if constexpr (BF == 64) finish_pair<EPI>(a, t, f0, q, total(q), total(q + 8));
+    else finish_one<EPI>(a, t, f0 + 4 * q, total(q));
 }
 
 // Split-K reduction + epilogue: thread (row t, 64-wide slab, q) sums the S
@@ -840,63 +985,7 @@ __global__ __launch_bounds__(256) void splitk_reduce(GemmArgs a, int S) {
             lo[e] = s < S ? lo[e] + pl[s][e] : lo[e];
             hi[e] = s < S ? hi[e] + ph[s][e] : hi[e];
         }
-    auto store_bf16 = [&](long col, f32x4 v) {
-        *(u32x2*)((bf16_t*)a.out + t * a.ldo + col) = u32x2{pack2(v[0], v[1]), pack2(v[2], v[3])};
-    };
-    const long c0 = a.col + slab + 4 * q;
-    if constexpr (EPI == JH_EPI_ROPE_BF16) {
-        if (slab < a.rope_cols) {
-            const long ps = (long)(a.pos[t] & 0xffff) * 32 + 4 * q;
-            const f32x4 c = *(const f32x4*)(a.cos_t + ps), sn = *(const f32x4*)(a.sin_t + ps);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float x0 = lo[e], x1 = hi[e];
-                lo[e] = x0 * c[e] - x1 * sn[e];
-                hi[e] = x1 * c[e] + x0 * sn[e];
-            }
-        }
-        store_bf16(c0, lo);
-        store_bf16(c0 + 32, hi);
-    } else if constexpr (EPI == JH_EPI_GEGLU_BF16) {
-        f32x4 g;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) g[e] = gelu_erf(lo[e]) * hi[e];
-        store_bf16(a.col + slab / 2 + 4 * q, g);
-    } else {
-        const bool biased = EPI == JH_EPI_BIAS_BF16 || EPI == JH_EPI_BIAS_RELU_BF16 || EPI == JH_EPI_BIAS_F32 ||
-                            (EPI == JH_EPI_RESID_F32 && a.bias);
-        if (biased) {
-            const f32x4 bl = *(const f32x4*)(a.bias + slab + 4 * q), bh = *(const f32x4*)(a.bias + slab + 32 + 4 * q);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                lo[e] += bl[e];
-                hi[e] += bh[e];
-                if constexpr (EPI == JH_EPI_BIAS_RELU_BF16) {
-                    lo[e] = fmaxf(lo[e], 0.0f);
-                    hi[e] = fmaxf(hi[e], 0.0f);
-                }
-            }
-        }
-        if constexpr (EPI == JH_EPI_RESID_F32 || EPI == JH_EPI_BIAS_F32) {
-            float* o = (float*)a.out + t * a.ldo + c0;
-            if constexpr (EPI == JH_EPI_RESID_F32) {
-                f32x4 ol = *(const f32x4*)o, oh = *(const f32x4*)(o + 32);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    ol[e] += lo[e];
-                    oh[e] += hi[e];
-                }
-                *(f32x4*)o = ol;
-                *(f32x4*)(o + 32) = oh;
-            } else {
-                *(f32x4*)o = lo;
-                *(f32x4*)(o + 32) = hi;
-            }
-        } else {
-            store_bf16(c0, lo);
-            store_bf16(c0 + 32, hi);
-        }
-    }
+    finish_pair<EPI>(a, t, slab, q, lo, hi);
 }
 
 // Tile shape: 128 features x 128 tokens, four waves of 64x64, two resident
@@ -927,12 +1016,6 @@ int splitk_count(const GemmArgs& a, long tiles) {
     return (kt + chunk - 1) / chunk;
 }
 
-// The one-launch small-batch kernel replaces split-K where split-K would run
-// automatically (workspace given, no forced split count) and K fits its LDS.
-bool use_small(const GemmArgs& a, long tiles) {
-    return a.partial && a.splits == 0 && a.k <= SMALL_KMAX && splitk_count(a, tiles) > 1;
-}
-
 // Workgroups of gemm_kernel resident at once on the current device (two per
 // CU), rounded down to a multiple of 8 XCDs; the persistent kernel's grid.
 int resident_tiles() {
@@ -950,15 +1033,60 @@ int resident_tiles() {
     return v;
 }
 
+// Tile width (64 or 32 features) of the one-launch small-batch kernel for
+// `a`, or 0 when launch_gemm does not use it.  It replaces split-K where
+// split-K would run automatically (workspace given, no forced split count)
+// and K fits its LDS; with the LayerNorm prologue it is the only kernel.
+// 32-feature tiles move fewer operand bytes per CU, so they are taken when
+// their workgroups fit one per CU (then for K up to 1152 as well), for the
+// epilogues without a 64-feature pairing.
+int small_bf(int epi, const GemmArgs& a) {
+    if (a.xf) return 64;
+    const long tiles = (long)((a.n + 127) / 128) * ((a.rows + 127) / 128);
+    if (!a.partial || a.splits != 0 || splitk_count(a, tiles) <= 1) return 0;
+    const bool paired = epi == JH_EPI_ROPE_BF16 || epi == JH_EPI_GEGLU_BF16;
+    const long wg32 = (long)(a.n / 32) * ((a.rows + SMALL_BT - 1) / SMALL_BT);
+    if (!paired && a.k <= small_kmax<32>() && wg32 <= resident_tiles() / 2) return 32;
+    return a.k <= small_kmax<64>() ? 64 : 0;
+}
+
+template <int EPI>
+void launch_small(const GemmArgs& a, int bf, hipStream_t s) {
+    constexpr bool PAIRED = EPI == JH_EPI_ROPE_BF16 || EPI == JH_EPI_GEGLU_BF16;
+    const dim3 grid((unsigned)((a.n / bf) * ((a.rows + SMALL_BT - 1) / SMALL_BT))), block(256);
+    if (a.xf) {
+        if constexpr (PAIRED || EPI == JH_EPI_STORE_BF16) {
+            switch (a.k) {
+                case 128: JH_LAUNCH((gemm_small_kernel<EPI, false, 64, 2>), grid, block, 0, s, a); break;
+                case 256: JH_LAUNCH((gemm_small_kernel<EPI, false, 64, 4>), grid, block, 0, s, a); break;
+                case 384: JH_LAUNCH((gemm_small_kernel<EPI, false, 64, 6>), grid, block, 0, s, a); break;
+                case 512: JH_LAUNCH((gemm_small_kernel<EPI, false, 64, 8>), grid, block, 0, s, a); break;
+                case 768: JH_LAUNCH((gemm_small_kernel<EPI, false, 64, 12>), grid, block, 0, s, a); break;
+                default: throw jh_error(1, "gemm: the LayerNorm prologue needs K = hidden in {128, 256, 384, 512, 768}");
+            }
+        } else {
+            throw jh_error(1, "gemm: the LayerNorm prologue supports the STORE, ROPE and GEGLU epilogues");
+        }
+    } else if (bf == 32) {
+        if constexpr (!PAIRED) {
+            if (a.gather) JH_LAUNCH((gemm_small_kernel<EPI, true, 32, 0>), grid, block, 0, s, a);
+            else JH_LAUNCH((gemm_small_kernel<EPI, false, 32, 0>), grid, block, 0, s, a);
+        } else {
+            throw jh_error(1, "gemm: paired epilogues need 64-feature tiles");
+        }
+    } else {
+        if (a.gather) JH_LAUNCH((gemm_small_kernel<EPI, true, 64, 0>), grid, block, 0, s, a);
+        else JH_LAUNCH((gemm_small_kernel<EPI, false, 64, 0>), grid, block, 0, s, a);
+    }
+    HIP_CHECK(hipGetLastError());
+}
+
 template <int EPI>
 void launch_cfg(const GemmArgs& a, hipStream_t s) {
     constexpr int BF = 128, BT = 128;
     const int blocks = ((a.n + BF - 1) / BF) * ((a.rows + BT - 1) / BT);
-    if (use_small(a, blocks)) {
-        const int sblocks = (a.n / SMALL_BF) * ((a.rows + SMALL_BT - 1) / SMALL_BT);
-        if (a.gather) JH_LAUNCH((gemm_small_kernel<EPI, true>), dim3(sblocks), dim3(256), 0, s, a);
-        else JH_LAUNCH((gemm_small_kernel<EPI, false>), dim3(sblocks), dim3(256), 0, s, a);
-        HIP_CHECK(hipGetLastError());
+    if (const int bf = small_bf(EPI, a)) {
+        launch_small<EPI>(a, bf, s);
         return;
     }
     const int S = splitk_count(a, blocks);
@@ -1029,9 +1157,18 @@ bool validate_gemm(int epi, const GemmArgs& a) {
     if (a.rows < 0 || a.n <= 0 || a.k <= 0 || a.k % BK || a.n % 64 || a.k > 8192)
         throw jh_error(1, "gemm: need K % 64 == 0, N % 64 == 0, K <= 8192");
     if (a.rows == 0) return false;
-    if (!a.x || !a.w || !a.out) throw jh_error(1, "gemm: null operand");
-    if (a.ldx % 8 || a.ldx < a.k || ((uintptr_t)a.x & 15) || ((uintptr_t)a.w & 15))
-        throw jh_error(1, "gemm: x/w must be 16-byte aligned with ldx % 8 == 0 and ldx >= K");
+    if (a.xf) {
+        // LayerNorm prologue: FP32 rows, 16-byte aligned, whole rows of K = hidden.
+        if (!a.w || !a.out || !a.ln_w) throw jh_error(1, "gemm: null operand");
+        if (a.gather || a.splits)
+            throw jh_error(1, "gemm: the LayerNorm prologue takes contiguous rows and no forced split-K");
+        if (a.k > small_kmax<64>() || a.ldx % 4 || a.ldx < a.k || ((uintptr_t)a.xf & 15) || ((uintptr_t)a.w & 15))
+            throw jh_error(1, "gemm: LayerNorm prologue needs K <= 768, 16-byte aligned rows, ldx % 4 == 0, ldx >= K");
+    } else {
+        if (!a.x || !a.w || !a.out) throw jh_error(1, "gemm: null operand");
+        if (a.ldx % 8 || a.ldx < a.k || ((uintptr_t)a.x & 15) || ((uintptr_t)a.w & 15))
+            throw jh_error(1, "gemm: x/w must be 16-byte aligned with ldx % 8 == 0 and ldx >= K");
+    }
     const bool f32out = epi == JH_EPI_RESID_F32 || epi == JH_EPI_BIAS_F32;
     const long width = epi == JH_EPI_GEGLU_BF16 ? a.n / 2 : a.n;
     const int per16 = f32out ? 4 : 8;  // elements per 16-byte store
@@ -1051,6 +1188,10 @@ bool validate_gemm(int epi, const GemmArgs& a) {
 int gemm_splitk_count(int epi, const GemmArgs& a) {
     if (!validate_gemm(epi, a)) return 1;
     return splitk_count(a, (long)((a.n + 127) / 128) * ((a.rows + 127) / 128));
+}
+
+bool gemm_uses_small(int epi, const GemmArgs& a) {
+    return validate_gemm(epi, a) && small_bf(epi, a) != 0;
 }
 
 void launch_gemm_partial(int epi, const GemmArgs& a, int splits, hipStream_t s) {

@@ -50,6 +50,14 @@ struct GemmArgs {
     int splits = 0;
     // set by launch_gemm for the split-K partial pass
     int kt_chunk = 0;
+    // LayerNorm prologue (one-launch small-batch kernel only): when xf is set,
+    // x is unused and the X operand is bf16(LN(xf row)) over K = hidden
+    // features, computed as layer_norm_kernel does; xf rows have stride ldx
+    // floats.  ln_b may be null.
+    const float* xf = nullptr;
+    const float* ln_w = nullptr;
+    const float* ln_b = nullptr;
+    float ln_eps = 0.0f;
 };
 
 void launch_gemm(int epilogue, const GemmArgs& a, hipStream_t stream);
@@ -57,6 +65,9 @@ void launch_gemm(int epilogue, const GemmArgs& a, hipStream_t stream);
 // partial pass alone (FP32 partials [splits][rows][n] into a.partial), for
 // callers that fuse the reduction with what follows (launch_resid_reduce_ln).
 int gemm_splitk_count(int epilogue, const GemmArgs& a);
+// Whether launch_gemm runs `a` as one launch of the small-batch kernel (the
+// only kernel with the LayerNorm prologue); false for rows == 0.
+bool gemm_uses_small(int epilogue, const GemmArgs& a);
 void launch_gemm_partial(int epilogue, const GemmArgs& a, int splits, hipStream_t stream);
 
 struct AttnTile {

@@ -7,87 +7,11 @@
 #include <hip/hip_runtime.h>
 
 #include "kernels.hpp"
+#include "rowvec.hpp"
 
 namespace {
 
 constexpr int ROWS_PER_BLOCK = 4;
-
-template <int EPL>
-struct RowVec {
-    static constexpr int VEC = EPL % 4 == 0 ? 4 : (EPL % 2 == 0 ? 2 : 1);
-    static constexpr int NC = EPL / VEC;  // vector chunks per lane
-    float v[EPL];
-
-    // Chunk c of this lane covers elements [(c*64 + lane)*VEC, +VEC).
-    __device__ static int index(int c, int lane) { return (c * 64 + lane) * VEC; }
-
-    __device__ void load(const float* row, int lane) {
-#pragma unroll
-        for (int c = 0; c < NC; ++c) {
-            const float* p = row + index(c, lane);
-            if constexpr (VEC == 4) {
-                f32x4 t = *(const f32x4*)p;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) v[c * 4 + e] = t[e];
-            } else if constexpr (VEC == 2) {
-                float2 t = *(const float2*)p;
-                v[c * 2] = t.x;
-                v[c * 2 + 1] = t.y;
-            } else {
-                v[c] = *p;
-            }
-        }
-    }
-    __device__ void store(float* row, int lane) const {
-#pragma unroll
-        for (int c = 0; c < NC; ++c) {
-            float* p = row + index(c, lane);
-            if constexpr (VEC == 4) {
-                *(f32x4*)p = f32x4{v[c * 4], v[c * 4 + 1], v[c * 4 + 2], v[c * 4 + 3]};
-            } else if constexpr (VEC == 2) {
-                *(float2*)p = make_float2(v[c * 2], v[c * 2 + 1]);
-            } else {
-                *p = v[c];
-            }
-        }
-    }
-    __device__ void store_bf16(bf16_t* row, int lane) const {
-#pragma unroll
-        for (int c = 0; c < NC; ++c) {
-            bf16_t* p = row + index(c, lane);
-            if constexpr (VEC == 4) {
-                *(u32x2*)p = u32x2{pack2(v[c * 4], v[c * 4 + 1]), pack2(v[c * 4 + 2], v[c * 4 + 3])};
-            } else if constexpr (VEC == 2) {
-                *(uint32_t*)p = pack2(v[c * 2], v[c * 2 + 1]);
-            } else {
-                *p = f2bf(v[c]);
-            }
-        }
-    }
-    // v = (v - mean) * rstd * w (+ b), two-pass statistics over the whole row.
-    __device__ void layer_norm(const float* w, const float* b, float eps, int lane) {
-        constexpr float inv_n = 1.0f / (EPL * 64);
-        float s = 0.0f;
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) s += v[e];
-        const float mean = wave_sum(s) * inv_n;
-        float q = 0.0f;
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) {
-            float d = v[e] - mean;
-            q += d * d;
-        }
-        const float rstd = 1.0f / __builtin_sqrtf(wave_sum(q) * inv_n + eps);
-        RowVec<EPL> g, bb;
-        g.load(w, lane);
-        if (b) bb.load(b, lane);
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) {
-            float y = (v[e] - mean) * rstd * g.v[e];
-            v[e] = b ? y + bb.v[e] : y;
-        }
-    }
-};
 
 template <int EPL>
 __global__ __launch_bounds__(256) void embed_ln_kernel(const uint32_t* __restrict__ ids, int rows,

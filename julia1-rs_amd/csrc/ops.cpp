@@ -44,6 +44,22 @@ int jh_op_gemm_splitk(int epilogue, const void* x, size_t ldx, const int32_t* ga
     });
 }
 
+int jh_op_gemm_ln(int epilogue, const float* xf, size_t ldx, size_t rows, const void* w, size_t n, size_t k,
+                  void* out, size_t ldo, size_t col, const int32_t* pos, const float* cos_t, const float* sin_t,
+                  size_t rope_cols, const float* ln_w, const float* ln_b, float eps, void* stream) {
+    return jh_guarded([&] {
+        if (!xf) throw jh_error(1, "gemm: null operand");
+        GemmArgs a{nullptr, (long)ldx, nullptr, as_int(rows, "rows"), (const bf16_t*)w, as_int(n, "n"),
+                   as_int(k, "k"), out, (long)ldo, as_int(col, "col"), nullptr, pos, cos_t, sin_t,
+                   as_int(rope_cols, "rope_cols")};
+        a.xf = xf;
+        a.ln_w = ln_w;
+        a.ln_b = ln_b;
+        a.ln_eps = eps;
+        launch_gemm(epilogue, a, (hipStream_t)stream);
+    });
+}
+
 // Gate/up interleave for the GEGLU epilogue (also used by jh_create): 64-row
 // block j holds gate rows [32j, 32j+32) then up rows [inter+32j, inter+32j+32).
 void jh_op_interleave_geglu(const float* wi, size_t inter, size_t k, float* out) {

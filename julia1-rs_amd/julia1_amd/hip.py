@@ -20,7 +20,8 @@ EXPORTS = (
     "jh_collect",
     "jh_set_graph", "jh_set_splitk", "jh_name", "jh_destroy", "jh_last_error", "jh_rope_table", "jh_debug_tokens",
     "jh_debug_encode", "jh_debug_workspace_limit", "jh_profile", "jh_profile_read", "jh_profile_replay",
-    "jh_op_gemm", "jh_op_gemm_splitk", "jh_op_gemm_splitk_noalloc", "jh_op_interleave_geglu", "jh_op_embed_ln", "jh_op_layer_norm", "jh_op_final_norm",
+    "jh_op_gemm", "jh_op_gemm_splitk", "jh_op_gemm_splitk_noalloc", "jh_op_gemm_ln", "jh_op_interleave_geglu",
+    "jh_op_embed_ln", "jh_op_layer_norm", "jh_op_final_norm",
     "jh_op_gather_f32", "jh_op_scorer", "jh_op_attention",
 )
 
@@ -74,6 +75,8 @@ def lib():
                                         C.c_int, vp]
         L.jh_op_gemm_splitk_noalloc.argtypes = [C.c_int, vp, sz, vp, sz, vp, sz, sz, vp, sz, sz, vp, vp, vp, vp,
                                                 sz, C.c_int, vp]
+        L.jh_op_gemm_ln.argtypes = [C.c_int, vp, sz, sz, vp, sz, sz, vp, sz, sz, vp, vp, vp, sz, vp, vp, C.c_float,
+                                    vp]
         L.jh_op_interleave_geglu.argtypes = [vp, sz, sz, vp]
         L.jh_op_interleave_geglu.restype = None
         L.jh_op_embed_ln.argtypes = [vp, sz, vp, vp, C.c_float, sz, vp, vp, vp]
@@ -236,6 +239,15 @@ def op_gemm_splitk(epi, x, w, out, workspace, splits=0, rows=None, gather=None, 
     check(lib().jh_op_gemm_splitk(epi, _dp(x), x.stride(0), _dp(gather), rows, _dp(w), n, k, _dp(out), out.stride(0),
                                   col, _dp(bias), _dp(pos), _dp(cos), _dp(sin), rope_cols, _dp(workspace),
                                   workspace.numel() * workspace.element_size(), splits, stream))
+
+
+def op_gemm_ln(epi, xf, w, out, ln_w, ln_b=None, eps=1e-5, rows=None, col=0, pos=None, cos=None, sin=None,
+               rope_cols=0, stream=None):
+    """jh_op_gemm_ln: X = bf16(LayerNorm(xf)) computed inside the GEMM; xf an FP32 torch tensor (2-D)."""
+    rows = xf.shape[0] if rows is None else rows
+    n, k = w.shape
+    check(lib().jh_op_gemm_ln(epi, _dp(xf), xf.stride(0), rows, _dp(w), n, k, _dp(out), out.stride(0), col,
+                              _dp(pos), _dp(cos), _dp(sin), rope_cols, _dp(ln_w), _dp(ln_b), eps, stream))
 
 
 def op_gemm_splitk_noalloc(epi, x, w, out, splits=0, rows=None, gather=None, col=0, bias=None, pos=None, cos=None,

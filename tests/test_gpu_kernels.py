@@ -246,9 +246,10 @@ def test_gemm_rope(theta):
                                  abi.EPI_BIAS_BF16, abi.EPI_BIAS_RELU_BF16, abi.EPI_BIAS_F32])
 def test_gemm_splitk_matches_f64(epi, splits, k, rows):
     """Small-batch GEMMs against the f64 product, with the same per-epilogue tolerances as the single-pass
-    GEMM, plus determinism: split-K (FP32 partials reduced in chunk order, then the epilogue) for K = 1152
-    or a forced split count, and the one-launch small-batch kernel (K split over the four waves of a
-    workgroup, reduced in wave order) for K <= 768 with the split count left to the library."""
+    GEMM, plus determinism: split-K (FP32 partials reduced in chunk order, then the epilogue) for a forced
+    split count and for the paired epilogues at K = 1152, and the one-launch small-batch kernel (K split
+    over the four waves of a workgroup, reduced in wave order) with the split count left to the library:
+    32-feature tiles up to K = 1152 for the unpaired epilogues, 64-feature tiles up to K = 768."""
     r = rng(12)
     n = 384
     x, w, ref = _gemm_inputs(r, rows, n, k)
@@ -312,6 +313,106 @@ def test_gemm_splitk_gathered_rows(splits):
     hip.op_gemm_splitk(abi.EPI_BIAS_F32, dev(x, BF16), dev(w, BF16), out, ws, splits=splits, rows=idx.size,
                        gather=dev(idx), bias=dev(np.zeros(256, dtype=np.float32)))
     assert np.abs(host(out) - ref[idx]).max() < 1e-5
+
+
+@pytest.mark.parametrize("rows,n,epi", [(300, 2304, abi.EPI_STORE_BF16), (300, 2304, abi.EPI_RESID_F32),
+                                        (300, 2304, abi.EPI_BIAS_F32), (130, 8192, abi.EPI_BIAS_RELU_BF16)])
+def test_gemm_small_wide_outputs(rows, n, epi):
+    """The one-launch small-batch kernel on 64-feature tiles for epilogues without a feature pairing (taken
+    when 32-feature tiles would not fit one workgroup per CU), against torch FP32."""
+    _check_small(rows, n, 768, epi, seed=rows + n + epi)
+
+
+def _check_small(rows, n, k, epi, seed):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    x = torch.randn(rows, k, device="cuda", generator=g).to(BF16)
+    w = (torch.randn(n, k, device="cuda", generator=g) * 0.02).to(BF16)
+    bias = torch.randn(n, device="cuda", generator=g) * 0.1
+    prod = x.float() @ w.float().T + (bias if epi != abi.EPI_STORE_BF16 else 0)
+    ws = torch.zeros(64 << 20, dtype=torch.uint8, device="cuda")
+    kw = dict(bias=bias) if epi != abi.EPI_STORE_BF16 else {}
+    if epi == abi.EPI_RESID_F32:
+        base = torch.randn(rows, n, device="cuda", generator=g)
+        out = base.clone()
+        hip.op_gemm_splitk(epi, x, w, out, ws, **kw)
+        torch.cuda.synchronize()
+        assert (out - (base + prod)).abs().max().item() < 1e-4
+        return
+    f32 = epi == abi.EPI_BIAS_F32
+    out = torch.zeros(rows, n, dtype=torch.float32 if f32 else BF16, device="cuda")
+    hip.op_gemm_splitk(epi, x, w, out, ws, **kw)
+    expect = prod.clamp_min(0.0) if epi == abi.EPI_BIAS_RELU_BF16 else prod
+    d = (out.float() - expect).abs()
+    if f32:
+        assert d.max().item() < 1e-4
+    else:
+        assert bool((d <= 4e-3 * expect.abs() + 1e-5).all()), d.max().item()
+
+
+@pytest.mark.parametrize("rows,hidden,n,epi,biased,pad", [
+    (128, 768, 2304, abi.EPI_ROPE_BF16, False, 0), (128, 768, 2304, abi.EPI_GEGLU_BF16, False, 0),
+    (160, 384, 1152, abi.EPI_ROPE_BF16, False, 0), (160, 384, 2304, abi.EPI_GEGLU_BF16, False, 0),
+    (1, 128, 384, abi.EPI_ROPE_BF16, True, 4), (33, 256, 512, abi.EPI_GEGLU_BF16, True, 0),
+    (70, 512, 1536, abi.EPI_ROPE_BF16, False, 8), (230, 768, 1152, abi.EPI_STORE_BF16, True, 0)])
+def test_gemm_layer_norm_prologue(rows, hidden, n, epi, biased, pad):
+    """The LayerNorm prologue of the small-batch GEMM gives the same bits as jh_op_layer_norm followed by the
+    same GEMM (bf16 operand, same K-slice order), for the hidden sizes it supports, LayerNorm with and without
+    bias, rows not a multiple of 32 and a row stride past K; plus torch FP32 of the same bf16 operand."""
+    g = torch.Generator(device="cuda").manual_seed(rows + hidden + n + epi)
+    xf_full = torch.randn(rows, hidden + pad, device="cuda", generator=g) * 3.0 + 0.5
+    xf = xf_full[:, :hidden]
+    ln_w = torch.rand(hidden, device="cuda", generator=g) + 0.5
+    ln_b = torch.randn(hidden, device="cuda", generator=g) * 0.1 if biased else None
+    w = (torch.randn(n, hidden, device="cuda", generator=g) * 0.02).to(BF16)
+    wk = dev(hip.interleave_geglu(w.float().cpu().numpy()), BF16) if epi == abi.EPI_GEGLU_BF16 else w
+    xn = torch.zeros(rows, hidden, dtype=BF16, device="cuda")
+    hip.op_layer_norm(xf.contiguous(), ln_w, ln_b, 1e-5, xn)
+    kw = {}
+    if epi == abi.EPI_ROPE_BF16:
+        pos = torch.randint(0, 8192, (rows,), device="cuda", generator=g, dtype=torch.int32)
+        cos, sin = (dev(t) for t in oracle.rope_table(160000.0, 8192))
+        kw = dict(pos=pos, cos=cos, sin=sin, rope_cols=2 * n // 3)
+    width = n // 2 if epi == abi.EPI_GEGLU_BF16 else n
+    got = torch.zeros(rows, width, dtype=BF16, device="cuda")
+    hip.op_gemm_ln(epi, xf_full, wk, got, ln_w, ln_b, 1e-5, rows=rows, **kw)
+    ref = torch.zeros_like(got)
+    ws = torch.zeros(64 << 20, dtype=torch.uint8, device="cuda")
+    hip.op_gemm_splitk(epi, xn, wk, ref, ws, **kw)
+    torch.cuda.synchronize()
+    if epi != abi.EPI_STORE_BF16:  # same kernel family and tile: identical
+        assert torch.equal(got, ref)
+    prod = xn.float() @ w.float().T
+    if epi == abi.EPI_GEGLU_BF16:
+        expect = torch.nn.functional.gelu(prod[:, :n // 2]) * prod[:, n // 2:]
+        scale = expect.abs() + 1e-3 * (prod[:, :n // 2] * prod[:, n // 2:]).abs()
+    elif epi == abi.EPI_ROPE_BF16:
+        rc = 2 * n // 3
+        expect, scale = prod.clone(), prod.abs().clone()
+        c, sn = kw["cos"][kw["pos"].long()], kw["sin"][kw["pos"].long()]
+        for hd in range(0, rc, 64):
+            a, b = prod[:, hd:hd + 32], prod[:, hd + 32:hd + 64]
+            expect[:, hd:hd + 32] = a * c - b * sn
+            expect[:, hd + 32:hd + 64] = b * c + a * sn
+            scale[:, hd:hd + 64] = (a.abs() + b.abs()).repeat(1, 2)
+    else:
+        expect, scale = prod, prod.abs()
+    d = (got.float() - expect).abs()
+    assert bool((d <= 4e-3 * scale + 1e-5).all()), d.max().item()
+
+
+def test_gemm_layer_norm_prologue_rejects():
+    xf = torch.zeros(4, 192, device="cuda")
+    w = torch.zeros(128, 192, dtype=BF16, device="cuda")
+    out = torch.zeros(4, 128, dtype=BF16, device="cuda")
+    ln_w = torch.ones(192, device="cuda")
+    with pytest.raises(hip.HipError):  # hidden 192 has no prologue instance
+        hip.op_gemm_ln(abi.EPI_STORE_BF16, xf, w, out, ln_w)
+    xf = torch.zeros(4, 128, device="cuda")
+    w = torch.zeros(128, 128, dtype=BF16, device="cuda")
+    with pytest.raises(hip.HipError):  # residual epilogue: not a prologue epilogue
+        hip.op_gemm_ln(abi.EPI_RESID_F32, xf, w, torch.zeros(4, 128, device="cuda"), ln_w[:128])
+    with pytest.raises(hip.HipError):  # no LayerNorm weights
+        hip.op_gemm_ln(abi.EPI_STORE_BF16, xf, w, out, None)
 
 
 def test_gemm_rejects_bad_shapes():
