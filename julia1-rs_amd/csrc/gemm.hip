@@ -24,6 +24,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <utility>
 
 #include "../../include/julia1_hip_ops.h"
 #include "kernels.hpp"
@@ -798,6 +799,14 @@ constexpr int small_kmax() {
     return SMALL_LDS / (BF + SMALL_BT) / 64 * 64;
 }
 
+// s_waitcnt vmcnt(N): all but this wave's N most recent vector-memory
+// operations (loads, DMA or stores) have completed.
+template <int N>
+__device__ inline void vmcnt() {
+    static_assert(N >= 0 && N <= 63, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
 // s_waitcnt vmcnt(n * PW), n in [0, SMALL_DEPTH]: all but this wave's DMA of
 // its last n issued segments (PW instructions each) has landed.
 template <int PW>
@@ -814,10 +823,15 @@ __device__ inline void wait_segments(int n) {
     }
 }
 
-template <int EPI, bool GATHER, int BF, int LN_EPL>
+template <int EPI, bool GATHER, int BF, int LN_EPL, int KSEG = 0>
 __global__ __launch_bounds__(256) void gemm_small_kernel(GemmArgs a) {
     constexpr int BT = SMALL_BT, FB = BF / 32, NCH = BF / 4;
     constexpr bool LNX = LN_EPL > 0;
+    // K/64 when known at compile time (the prologue's hidden size, or the
+    // instance's K): the segment loop is then unrolled with every wait count an
+    // immediate, which at two MFMAs per wave per segment is measurably faster
+    // than the loop with a computed wait.
+    constexpr int CSEG = LNX ? LN_EPL : KSEG;
     constexpr int WI = BF / 8, XI = LNX ? 0 : BT / 8;  // DMA instructions (8 rows x 128 B) per K segment
     constexpr int PW = (WI + XI) / 4;                  // ... per wave
     static_assert((WI + XI) % 4 == 0 && (BF == 64 || BF == 32), "tile shape");
@@ -826,7 +840,7 @@ __global__ __launch_bounds__(256) void gemm_small_kernel(GemmArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int nF = a.n / BF;
     const int f0 = (int)(blockIdx.x % nF) * BF, t0 = (int)(blockIdx.x / nF) * BT;
-    const int nseg = a.k / 64;  // 128-byte row segments
+    const int nseg = CSEG ? CSEG : a.k / 64;  // 128-byte row segments
     bf16_t* const sW = smem;                   // segment g: rows [0, BF) at sW + g*BF*64
     bf16_t* const sX = smem + nseg * BF * 64;  // segment g: rows [0, BT) at sX + g*BT*64
     const i32x4 rw = make_rsrc(a.w + (long)f0 * a.k, (uint64_t)BF * a.k * 2);
@@ -909,16 +923,34 @@ __global__ __launch_bounds__(256) void gemm_small_kernel(GemmArgs a) {
     for (int i = 0; i < FB; ++i)
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[i][e] = 0.0f;
-    for (int g = 0; g < nseg; ++g) {
-        wait_segments<PW>(issued - g - 1);  // this wave's part of segment g has landed
-        __syncthreads();                     // ... and every wave's
-        if (issued < nseg) issue(issued++);
+    auto multiply = [&](int g) {
         const bf16x8 bx = *(const bf16x8*)&sX[g * BT * 64 + lr * 64 + ((c ^ swz(lr)) * 8)];
 #pragma unroll
         for (int i = 0; i < FB; ++i) {
             const int r = i * 32 + lr;
             const bf16x8 af = *(const bf16x8*)&sW[g * BF * 64 + r * 64 + ((c ^ swz(r)) * 8)];
             acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, bx, acc[i], 0, 0, 0);
+        }
+    };
+    if constexpr (CSEG > 0) {
+        constexpr int NSEG = CSEG, ISSUED0 = NSEG < SMALL_DEPTH ? NSEG : SMALL_DEPTH;
+        [&]<int... G>(std::integer_sequence<int, G...>) {
+            (
+                [&] {
+                    constexpr int ISSUED = ISSUED0 + G < NSEG ? ISSUED0 + G : NSEG;
+                    vmcnt<PW * (ISSUED - G - 1)>();  // this wave's part of segment G has landed
+                    __syncthreads();                 // ... and every wave's
+                    if constexpr (ISSUED < NSEG) issue(ISSUED);
+                    multiply(G);
+                }(),
+                ...);
+        }(std::make_integer_sequence<int, NSEG>{});
+    } else {
+        for (int g = 0; g < nseg; ++g) {
+            wait_segments<PW>(issued - g - 1);  // this wave's part of segment g has landed
+            __syncthreads();                     // ... and every wave's
+            if (issued < nseg) issue(issued++);
+            multiply(g);
         }
     }
     __syncthreads();  // operand LDS is free: reused for the partial tiles
@@ -1070,12 +1102,17 @@ void launch_small(const GemmArgs& a, int bf, hipStream_t s) {
     } else if (bf == 32) {
         if constexpr (!PAIRED) {
             if (a.gather) JH_LAUNCH((gemm_small_kernel<EPI, true, 32, 0>), grid, block, 0, s, a);
+            else if (a.k == 384) JH_LAUNCH((gemm_small_kernel<EPI, false, 32, 0, 6>), grid, block, 0, s, a);
+            else if (a.k == 768) JH_LAUNCH((gemm_small_kernel<EPI, false, 32, 0, 12>), grid, block, 0, s, a);
+            else if (a.k == 1152) JH_LAUNCH((gemm_small_kernel<EPI, false, 32, 0, 18>), grid, block, 0, s, a);
             else JH_LAUNCH((gemm_small_kernel<EPI, false, 32, 0>), grid, block, 0, s, a);
         } else {
             throw jh_error(1, "gemm: paired epilogues need 64-feature tiles");
         }
     } else {
         if (a.gather) JH_LAUNCH((gemm_small_kernel<EPI, true, 64, 0>), grid, block, 0, s, a);
+        else if (a.k == 384) JH_LAUNCH((gemm_small_kernel<EPI, false, 64, 0, 6>), grid, block, 0, s, a);
+        else if (a.k == 768) JH_LAUNCH((gemm_small_kernel<EPI, false, 64, 0, 12>), grid, block, 0, s, a);
         else JH_LAUNCH((gemm_small_kernel<EPI, false, 64, 0>), grid, block, 0, s, a);
     }
     HIP_CHECK(hipGetLastError());

@@ -241,7 +241,7 @@ def test_gemm_rope(theta):
 
 
 @pytest.mark.parametrize("splits,k,rows", [(0, 1152, 70), (2, 1152, 70), (5, 1152, 70),
-                                           (0, 768, 70), (0, 384, 1), (0, 384, 33)])
+                                           (0, 768, 70), (0, 384, 1), (0, 384, 33), (0, 512, 70), (0, 128, 5)])
 @pytest.mark.parametrize("epi", [abi.EPI_STORE_BF16, abi.EPI_ROPE_BF16, abi.EPI_GEGLU_BF16, abi.EPI_RESID_F32,
                                  abi.EPI_BIAS_BF16, abi.EPI_BIAS_RELU_BF16, abi.EPI_BIAS_F32])
 def test_gemm_splitk_matches_f64(epi, splits, k, rows):
