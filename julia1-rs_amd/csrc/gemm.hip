@@ -52,10 +52,11 @@ __device__ constexpr int oswz(int r) {
 // Epilogue of one wave's 64 x (32·TB) tile (features fw0.., tokens tw0..).
 // acc[i][j][e] holds feature fw0 + i*32 + (e/4)*8 + g4 + e%4 of token
 // tw0 + j*32 + lr.  Phase 1 applies the elementwise part in registers and
-// writes FP32 results to the wave's staging rows in LDS ([token][column]);
-// phase 2 reads them back along rows so each store instruction writes whole
-// 128/256-byte row segments (8 or 4 rows per instruction) instead of 32
-// scattered 16-byte pieces.
+// writes the results to the wave's staging rows in LDS ([token][column]):
+// FP32 for the FP32 outputs, already rounded to bf16 for the bf16 outputs
+// (the same rounding of the same values, at half the LDS traffic); phase 2
+// reads them back along rows so each store instruction writes whole
+// 64/128/256-byte row segments instead of 32 scattered pieces.
 template <int EPI, int TB = 2>
 __device__ inline void epilogue(const GemmArgs& a, f32x16 (&acc)[2][TB], int fw0, int tw0, int lane, float* stage,
                                 const f32x4* rope_c = nullptr, const f32x4* rope_s = nullptr) {
@@ -67,6 +68,16 @@ __device__ inline void epilogue(const GemmArgs& a, f32x16 (&acc)[2][TB], int fw0
     constexpr int CPR = OW / 4;          // 16-byte FP32 chunks per staging row
     const int g4 = (lane >> 5) * 4, lr = lane & 31;
     auto put = [&](int row, int chunk, f32x4 v) { *(f32x4*)&stage[row * OW + ((chunk ^ oswz<CPR>(row)) * 4)] = v; };
+    // bf16 staging rows: OW/8 16-byte chunks, XOR-swizzled by the row so that
+    // the 8-byte writes of 64 lanes (32 rows x 2 halves of one chunk) and the
+    // 16-byte row reads of each quarter-wave both spread over all banks.
+    constexpr int BCPR = OW / 8;
+    bf16_t* const bstage = (bf16_t*)stage;
+    auto bswz = [](int r) { return BCPR == 8 ? (r >> 1) & 7 : (r >> 2) & 3; };
+    auto putb = [&](int row, int fl, f32x4 v) {  // columns fl .. fl+3, fl % 4 == 0
+        *(u32x2*)&bstage[row * OW + (((fl >> 3) ^ bswz(row)) * 8) + (fl & 4)] =
+            u32x2{pack2(v[0], v[1]), pack2(v[2], v[3])};
+    };
     const long col0 = a.col + (GEGLU ? fw0 / 2 : fw0);
 
     // Residual: all 16 of this lane's old FP32 chunks are loaded before the
@@ -108,8 +119,8 @@ __device__ inline void epilogue(const GemmArgs& a, f32x16 (&acc)[2][TB], int fw0
                         hi[e] = x1 * c[e] + x0 * s[e];
                     }
                 }
-                put(tl, d / 4, lo);
-                put(tl, 8 + d / 4, hi);
+                putb(tl, d, lo);
+                putb(tl, 32 + d, hi);
             }
         } else if constexpr (GEGLU) {
             // Rows [fw0, fw0+32) are gate, [fw0+32, fw0+64) up, for outputs fw0/2 + [0, 32).
@@ -119,7 +130,7 @@ __device__ inline void epilogue(const GemmArgs& a, f32x16 (&acc)[2][TB], int fw0
                 f32x4 g;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) g[e] = gelu_erf(acc[0][j][qd * 4 + e]) * acc[1][j][qd * 4 + e];
-                put(tl, d / 4, g);
+                putb(tl, d, g);
             }
         } else {
 #pragma unroll
@@ -138,7 +149,8 @@ __device__ inline void epilogue(const GemmArgs& a, f32x16 (&acc)[2][TB], int fw0
                             if constexpr (EPI == JH_EPI_BIAS_RELU_BF16) v[e] = fmaxf(v[e], 0.0f);
                         }
                     }
-                    put(tl, fl / 4, v);
+                    if constexpr (F32OUT) put(tl, fl / 4, v);
+                    else putb(tl, fl, v);
                 }
         }
     }
@@ -164,16 +176,14 @@ __device__ inline void epilogue(const GemmArgs& a, f32x16 (&acc)[2][TB], int fw0
         }
     } else {
         // OW/8 lanes per bf16 output row (16 bytes each), 64/(OW/8) rows per pass.
-        constexpr int LPR = OW / 8, RPP = 64 / LPR;
+        constexpr int LPR = BCPR, RPP = 64 / LPR;
         const int q = lane % LPR;
 #pragma unroll 4
         for (int rr = lane / LPR; rr < ROWS; rr += RPP) {
             const int t = tw0 + rr;
             if (t >= a.rows) break;
-            const f32x4 v0 = *(const f32x4*)&stage[rr * OW + (((2 * q) ^ oswz<CPR>(rr)) * 4)];
-            const f32x4 v1 = *(const f32x4*)&stage[rr * OW + (((2 * q + 1) ^ oswz<CPR>(rr)) * 4)];
             *(u32x4*)((bf16_t*)a.out + (long)t * a.ldo + col0 + q * 8) =
-                u32x4{pack2(v0[0], v0[1]), pack2(v0[2], v0[3]), pack2(v1[0], v1[1]), pack2(v1[2], v1[3])};
+                *(const u32x4*)&bstage[rr * OW + ((q ^ bswz(rr)) * 8)];
         }
     }
 }
@@ -526,20 +536,35 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
 // all of a step's DMA, and waves 4-7, which share those SIMDs, start their
 // MFMAs at once; waves 0-3 compute after their burst, while 4-7 wait at the
 // next barrier.  The tile moves half the operand bytes per MFMA of a
-// 128x128 tile.  Each wave stages its epilogue through 8 KB of the last
-// step's buffers (plus a slack block when those are smaller than 64 KB).
-// Same products in the same K order as gemm_kernel: results are identical.
+// 128x128 tile.  Each wave stages its epilogue through 8 KB (FP32 outputs)
+// or 4 KB (bf16 outputs) of the last step's buffers, plus a slack block when
+// those are too small.  Same products in the same K order as gemm_kernel:
+// results are identical.
+//
+// RoPE with 192-token tiles: the tile's cos/sin table rows (192 tokens x 32
+// f32 each, 48 KB) are gathered into LDS by the loader waves' DMA during the
+// second-to-last K step, and every wave's epilogue reads them from there.
+// Loaded from global memory by each wave instead, the four feature waves of a
+// token block would each fetch the same rows: 192 KB per tile through the
+// texture addresser, twice the tile's output bytes, with the epilogue waiting
+// on them (measured: 5.3-5.9 us per tile against 2.2-2.9 us for a plain store).
 template <int EPI, int BT>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void gemm_big_kernel(GemmArgs a) {
     constexpr int BF = 256, FB = 2, TB = BT / 64;
     constexpr int NW = BF / 32, NX = BT / 32;          // DMA instructions per loader wave and stage (W, X)
     constexpr int WSTAGE = BF * BK, XSTAGE = BT * BK;  // bf16 elements per stage
-    constexpr int STG = 4096;                           // bf16 elements (8 KB) of staging per wave
+    constexpr bool F32OUT = EPI == JH_EPI_RESID_F32 || EPI == JH_EPI_BIAS_F32;
+    constexpr int STG = F32OUT ? 4096 : 2048;           // bf16 elements of staging per wave
     constexpr int SLACK = 8 * STG > WSTAGE + XSTAGE ? 8 * STG - (WSTAGE + XSTAGE) : 0;
-    __shared__ __align__(1024) bf16_t smem[2 * WSTAGE + 2 * XSTAGE + SLACK];
+    constexpr bool RLDS = EPI == JH_EPI_ROPE_BF16 && BT == 192;  // cos/sin rows staged in LDS
+    constexpr int CSROWS = RLDS ? BT : 0;                        // 128-byte table rows per table
+    constexpr int NCS = CSROWS / 8 / 4;                          // DMA instructions per loader wave per table
+    __shared__ __align__(1024) bf16_t smem[2 * WSTAGE + 2 * XSTAGE + SLACK + 2 * CSROWS * 64];
     bf16_t* const sW = smem;
     bf16_t* const sX = smem + 2 * WSTAGE;
     bf16_t* const sSlack = smem + 2 * WSTAGE + 2 * XSTAGE;
+    float* const sCos = (float*)(sSlack + SLACK);  // [CSROWS][32], 16-byte chunks swizzled by swz(row)
+    float* const sSin = sCos + CSROWS * 32;
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const bool loader = wave < 4;
     const int nF = (a.n + BF - 1) / BF, nTk = (a.rows + BT - 1) / BT, ntiles = nF * nTk;
@@ -613,15 +638,60 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
         // prefetch their registers do not fit two waves per SIMD.)
         constexpr bool ROPE = EPI == JH_EPI_ROPE_BF16 && TB <= 3;
         const bool rot = ROPE && f0 + wf * 64 < a.rope_cols;
-        int rp[ROPE ? TB : 1];
-        if constexpr (ROPE) {
+        constexpr bool RGLB = ROPE && !RLDS;  // cos/sin loaded from global memory by each wave
+        int rp[RGLB ? TB : 1];
+        if constexpr (RGLB) {
 #pragma unroll
             for (int j = 0; j < TB; ++j)
                 rp[j] = rot ? (a.pos[min(t0 + wt * (BT / 2) + j * 32 + lr, a.rows - 1)] & 0xffff) * 32 : 0;
         }
+        // RLDS: loader wave w gathers table rows [NCS*8*w, NCS*8*(w+1)) of the
+        // tile's tokens, lane i row 8j + i/8 of its instruction j, the 16-byte
+        // chunk that belongs in slot i%8 of that row under the swizzle.
+        const bool rot_tile = RLDS && loader && f0 < a.rope_cols;
+        uint32_t csoff[RLDS ? NCS : 1];
+        if constexpr (RLDS) {
+            if (rot_tile) {
+#pragma unroll
+                for (int j = 0; j < NCS; ++j) {
+                    const int r = (wave * NCS + j) * 8 + (lane >> 3);
+                    csoff[j] = (uint32_t)(a.pos[min(t0 + r, a.rows - 1)] & 0xffff) * 128 +
+                               (uint32_t)(((lane & 7) ^ swz(r)) * 16);
+                }
+            }
+        }
+        auto rope_dma = [&]() {
+            if constexpr (RLDS) {
+                if (rot_tile) {
+                    const i32x4 rcos = make_rsrc(a.cos_t, 65536ull * 128), rsin = make_rsrc(a.sin_t, 65536ull * 128);
+#pragma unroll
+                    for (int j = 0; j < NCS; ++j) {
+                        const uint32_t lc = __builtin_amdgcn_readfirstlane(
+                            (uint32_t)(uintptr_t)&sCos[(wave * NCS + j) * 8 * 32]);
+                        const uint32_t ls = __builtin_amdgcn_readfirstlane(
+                            (uint32_t)(uintptr_t)&sSin[(wave * NCS + j) * 8 * 32]);
+                        asm volatile("buffer_load_dwordx4 %1, %2, %3 offen lds" ::"{m0}"(lc), "v"(csoff[j]),
+                                     "s"(rcos), "s"(0)
+                                     : "memory");
+                        asm volatile("buffer_load_dwordx4 %1, %2, %3 offen lds" ::"{m0}"(ls), "v"(csoff[j]),
+                                     "s"(rsin), "s"(0)
+                                     : "memory");
+                    }
+                }
+            }
+        };
         f32x4 rc[4], rs[4];
         auto rope_load = [&](int j) {
-            if constexpr (ROPE) {
+            if constexpr (RLDS) {
+                if (rot) {
+                    const int r = wt * (BT / 2) + j * 32 + lr;
+#pragma unroll
+                    for (int qd = 0; qd < 4; ++qd) {
+                        rc[qd] = *(const f32x4*)&sCos[r * 32 + ((qd * 2 + lg) ^ swz(r)) * 4];
+                        rs[qd] = *(const f32x4*)&sSin[r * 32 + ((qd * 2 + lg) ^ swz(r)) * 4];
+                    }
+                }
+            } else if constexpr (ROPE) {
                 if (rot) {
 #pragma unroll
                     for (int qd = 0; qd < 4; ++qd) {
@@ -642,10 +712,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
             const int st = (base + kt) & 1;
             if (kt > 0 || first) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             __syncthreads();
-            if (kt + 1 == KT) rope_load(0);
+            if (!RLDS && kt + 1 == KT) rope_load(0);
             if (loader) {
                 if (kt + 1 < KT) issue(sc, kt + 1, st ^ 1);
                 else if (has_next) issue(sn, 0, st ^ 1);
+                // waited for at the next step's start (or before the epilogue when KT == 1)
+                if (kt == (KT >= 2 ? KT - 2 : 0)) rope_dma();
             }
             const bf16_t* W = sW + st * WSTAGE;
             const bf16_t* X = sX + st * XSTAGE;
@@ -679,10 +751,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
             }
         }
         const int st_last = (base + KT - 1) & 1;
+        // With one K step the cos/sin rows were issued in it: they land before the barrier.
+        if (RLDS && KT == 1 && loader) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();  // every wave is done reading the last step's buffers
         if (has_next) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        // 8 KB of staging per wave: the last step's W buffer, then its X
-        // buffer, then the slack block.
+        if constexpr (RLDS) rope_load(0);
+        // Staging per wave: the last step's W buffer, then its X buffer, then
+        // the slack block.
         const int so = wave * STG;
         bf16_t* const sbase = so < WSTAGE ? sW + st_last * WSTAGE + so
                               : so < WSTAGE + XSTAGE ? sX + st_last * XSTAGE + (so - WSTAGE)
