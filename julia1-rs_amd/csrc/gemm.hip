@@ -567,15 +567,25 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
     float* const sSin = sCos + CSROWS * 32;
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const bool loader = wave < 4;
-    const int nF = (a.n + BF - 1) / BF, nTk = (a.rows + BT - 1) / BT, ntiles = nF * nTk;
-    auto coords = [&](int b, int& f0, int& t0) {
+    // Token tiles come in two phases: rows [0, mix) in BT-token tiles, then
+    // (mix > 0) the rest in (BT-32)-token tiles, so that the last round of
+    // resident workgroups carries smaller tiles instead of leaving CUs idle.
+    // Each phase is dealt as its own round-robin over the grid.
+    const int nF = (a.n + BF - 1) / BF;
+    const int mix = a.mix_rows;
+    const int nT[2] = {((mix > 0 ? mix : a.rows) + BT - 1) / BT, mix > 0 ? (a.rows - mix + BT - 33) / (BT - 32) : 0};
+    const int nTiles[2] = {nF * nT[0], nF * nT[1]};
+    // Tile b of phase ph: f0, t0 and its token height ht.
+    auto coords = [&](int ph, int b, int& f0, int& t0, int& ht) {
+        const int ntiles = nTiles[ph], nTk = nT[ph];
+        ht = ph ? BT - 32 : BT;
         const int xcd = b & 7, local = b >> 3, q8 = ntiles >> 3, r8 = ntiles & 7;
         const int tile = xcd * q8 + (xcd < r8 ? xcd : r8) + local;
         constexpr int GROUP = 4;
         const int grp = tile / (GROUP * nF), gi = tile - grp * GROUP * nF;
         const int gh = min(GROUP, nTk - grp * GROUP);
         f0 = (gi / gh) * BF;
-        t0 = (grp * GROUP + gi % gh) * BT;
+        t0 = (ph ? mix : 0) + (grp * GROUP + gi % gh) * ht;
     };
     // Loader wave w's instruction j fills operand rows 32j + 8w .. +7 (lane i:
     // row 32j + 8w + i/8, swizzled chunk); rows past the end of W or X fall
@@ -594,7 +604,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
     const uint32_t wstep = 32u * a.k * 2, xstep = 32u * (uint32_t)a.ldx * 2;  // bytes per 32 rows
     const uint32_t wl0 = (uint32_t)(uintptr_t)&sW[(wave & 3) * 8 * 64];
     const uint32_t xl0 = (uint32_t)(uintptr_t)&sX[(wave & 3) * 8 * 64];
-    auto issue = [&](const Src& s, int kt, int st) {
+    // X rows [ht, BT) of a short tile are not loaded.
+    auto issue = [&](const Src& s, int kt, int st, int ht) {
         const uint32_t kb = (uint32_t)kt * BK * 2;
 #pragma unroll
         for (int j = 0; j < (NW > NX ? NW : NX); ++j) {
@@ -604,7 +615,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
                              "s"(s.rw), "s"(kb)
                              : "memory");
             }
-            if (j < NX) {
+            if (j < NX && (j < NX - 1 || ht == BT)) {
                 const uint32_t lx = __builtin_amdgcn_readfirstlane(xl0 + (st * XSTAGE + j * 32 * 64) * 2);
                 asm volatile("buffer_load_dwordx4 %1, %2, %3 offen lds" ::"{m0}"(lx), "v"(xoff + j * xstep),
                              "s"(s.rx), "s"(kb)
@@ -612,24 +623,33 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
             }
         }
     };
-    const int wf = wave & 3, wt = wave >> 2, lr = lane & 31, lg = lane >> 5;
+    const int wf = wave & 3, lr = lane & 31, lg = lane >> 5;
     const int G = gridDim.x, KT = a.k / BK;
-    int cur = blockIdx.x, f0, t0, base = 0;
-    if (cur >= ntiles) return;
-    coords(cur, f0, t0);
+    // Waves 0-3 multiply the tile's first 32·TB tokens (32·(TB-1) on a short
+    // tile), waves 4-7 the next 32·TB.
+    int ph = 0, cur = blockIdx.x, f0, t0, ht, base = 0;
+    if (cur >= nTiles[0]) {
+        ph = 1;
+        if (cur >= nTiles[1]) return;
+    }
+    coords(ph, cur, f0, t0, ht);
     Src sc;
     setup(f0, t0, sc);
-    if (loader) issue(sc, 0, 0);
+    if (loader) issue(sc, 0, 0, ht);
     bool first = true;
     while (true) {
-        const int nxt = cur + G;
-        const bool has_next = nxt < ntiles;
-        int nf0 = 0, nt0 = 0;
+        int nph = ph, nxt = cur + G;
+        if (nxt >= nTiles[ph] && ph == 0) nph = 1, nxt = blockIdx.x;
+        const bool has_next = nxt < nTiles[nph];
+        int nf0 = 0, nt0 = 0, nht = BT;
         Src sn = sc;
         if (has_next) {
-            coords(nxt, nf0, nt0);
+            coords(nph, nxt, nf0, nt0, nht);
             setup(nf0, nt0, sn);
         }
+        const int lb = ht == BT ? TB : TB - 1;           // 32-token blocks of the loader waves
+        const int toff = loader ? 0 : lb * 32;          // this wave's first token in the tile
+        const bool full = !loader || ht == BT;          // this wave multiplies all TB blocks
         // RoPE: this lane's token positions are loaded at the tile's start and
         // the first 32-token block's cos/sin values during the last K step,
         // so the epilogue, which every wave of the CU runs at once, does not
@@ -643,7 +663,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
         if constexpr (RGLB) {
 #pragma unroll
             for (int j = 0; j < TB; ++j)
-                rp[j] = rot ? (a.pos[min(t0 + wt * (BT / 2) + j * 32 + lr, a.rows - 1)] & 0xffff) * 32 : 0;
+                rp[j] = rot ? (a.pos[min(t0 + toff + j * 32 + lr, a.rows - 1)] & 0xffff) * 32 : 0;
         }
         // RLDS: loader wave w gathers table rows [NCS*8*w, NCS*8*(w+1)) of the
         // tile's tokens, lane i row 8j + i/8 of its instruction j, the 16-byte
@@ -684,7 +704,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
         auto rope_load = [&](int j) {
             if constexpr (RLDS) {
                 if (rot) {
-                    const int r = wt * (BT / 2) + j * 32 + lr;
+                    const int r = toff + j * 32 + lr;
 #pragma unroll
                     for (int qd = 0; qd < 4; ++qd) {
                         rc[qd] = *(const f32x4*)&sCos[r * 32 + ((qd * 2 + lg) ^ swz(r)) * 4];
@@ -714,8 +734,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
             __syncthreads();
             if (!RLDS && kt + 1 == KT) rope_load(0);
             if (loader) {
-                if (kt + 1 < KT) issue(sc, kt + 1, st ^ 1);
-                else if (has_next) issue(sn, 0, st ^ 1);
+                if (kt + 1 < KT) issue(sc, kt + 1, st ^ 1, ht);
+                else if (has_next) issue(sn, 0, st ^ 1, nht);
                 // waited for at the next step's start (or before the epilogue when KT == 1)
                 if (kt == (KT >= 2 ? KT - 2 : 0)) rope_dma();
             }
@@ -731,7 +751,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
                 }
 #pragma unroll
                 for (int j = 0; j < TB; ++j) {
-                    const int r = wt * (BT / 2) + j * 32 + lr;
+                    const int r = toff + j * 32 + lr;
                     bx[s][j] = *(const bf16x8*)&X[r * BK + ((c ^ swz(r)) * 8)];
                 }
             };
@@ -745,7 +765,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
                 for (int i = 0; i < FB; ++i)
 #pragma unroll
                     for (int j = 0; j < TB; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[s][i], bx[s][j], acc[i][j], 0, 0, 0);
+                        if (j < TB - 1 || full)
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[s][i], bx[s][j], acc[i][j], 0, 0, 0);
                 __builtin_amdgcn_sched_barrier(0);
                 if (ks + 2 < BK / 16) load(ks + 2, s);
             }
@@ -766,19 +787,22 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
         if (f0 + wf * 64 < a.n) {
 #pragma unroll
             for (int j = 0; j < TB; ++j) {
+                if (j == TB - 1 && !full) break;
                 f32x16 part[2][1] = {{acc[0][j]}, {acc[1][j]}};
                 if constexpr (ROPE) {
                     if (j > 0) rope_load(j);
-                    epilogue<EPI, 1>(a, part, f0 + wf * 64, t0 + wt * (BT / 2) + j * 32, lane, stg, rc, rs);
+                    epilogue<EPI, 1>(a, part, f0 + wf * 64, t0 + toff + j * 32, lane, stg, rc, rs);
                 } else {
-                    epilogue<EPI, 1>(a, part, f0 + wf * 64, t0 + wt * (BT / 2) + j * 32, lane, stg);
+                    epilogue<EPI, 1>(a, part, f0 + wf * 64, t0 + toff + j * 32, lane, stg);
                 }
             }
         }
         if (!has_next) break;
+        ph = nph;
         cur = nxt;
         f0 = nf0;
         t0 = nt0;
+        ht = nht;
         sc = sn;
         base = (base + KT) & 1;
         first = false;
@@ -1193,6 +1217,68 @@ void launch_small(const GemmArgs& a, int bf, hipStream_t s) {
     HIP_CHECK(hipGetLastError());
 }
 
+// Which kernel launch_gemm runs for `a` (past the small-batch and split-K
+// paths) and its tile geometry: BF features x BT tokens per tile, token blocks
+// grouped GROUP at a time, `grid` workgroups; for the eight-wave kernel, the
+// rows [0, mix) in BT-token tiles and the rest in (BT-32)-token tiles.
+struct GemmPlan {
+    enum Kind { PLAIN, PERSIST, BIG } kind;
+    int bf, bt, group, grid, mix;
+};
+
+GemmPlan plan_gemm(const GemmArgs& a) {
+    constexpr int BF = 128, BT = 128;
+    const int blocks = ((a.n + BF - 1) / BF) * ((a.rows + BT - 1) / BT);
+    const int resident = resident_tiles();
+    if (a.gather || blocks <= resident) return {GemmPlan::PLAIN, 128, 128, 8, blocks, 0};
+    // More tiles than resident workgroups.  Each candidate is costed as its
+    // rounds of resident workgroups times the time one round took on
+    // MI355X (K = 768, N = 2304, one box): persistent 128x128 12.9 us and
+    // 128x192 20.6 us at two workgroups per CU; eight-wave 256x192 19.0
+    // and 256x256 22.4 us at one per CU.  A round of eight-wave tiles 32
+    // tokens shorter costs ~6% less (the operand DMA, which bounds the K
+    // loop, still moves the same W slice per step): 17.9 and 21.1 us.
+    auto rounds = [](long tiles, long slots) { return (tiles + slots - 1) / slots; };
+    const long t192 = (long)((a.n + 127) / 128) * ((a.rows + 191) / 192);
+    const long r128 = rounds(blocks, resident), r192 = rounds(t192, resident);
+    // Persistent 128-feature tiles: 192 tokens when their rounds, at 1.5x
+    // the work each, cost no more than the 128-token tiles' rounds.
+    const bool p192 = t192 >= resident && 3 * r192 <= 2 * r128;
+    double best = p192 ? r192 * 20.6 : r128 * 12.9;
+    int big = 0;
+    long mix = 0;
+    if (a.n >= 1024) {
+        const int grid = resident / 2;
+        const long nF = (a.n + 255) / 256;
+        // (256x128 never beats the persistent 128x128 tiles: it has at least
+        // their rounds at a higher cost per round.)
+        const int bts[2] = {256, 192};
+        const double per_round[2] = {22.4, 19.0}, per_short[2] = {21.1, 17.9};
+        for (int c = 0; c < 2; ++c) {
+            const int bt = bts[c];
+            const long nT = (a.rows + bt - 1) / bt;
+            const double cost = rounds(nF * nT, grid) * per_round[c];
+            if (cost < best) best = cost, big = bt, mix = 0;
+            // na full-height token blocks, then the rest in shorter ones, so
+            // the second round carries smaller tiles instead of idle CUs
+            // (measured for two rounds; more are left uniform).
+            for (long na = nT - 1; na >= 1; --na) {
+                const long nb = (a.rows - na * bt + bt - 33) / (bt - 32);
+                if (nF * na > grid || nF * nb > grid) continue;
+                const double cm = per_round[c] + per_short[c];
+                if (cm < best) best = cm, big = bt, mix = na * bt;
+            }
+        }
+    }
+    if (big) {
+        const long nF = (a.n + 255) / 256;
+        const long tiles = mix ? nF * std::max(mix / big, (a.rows - mix + big - 33) / (big - 32))
+                               : nF * ((a.rows + big - 1) / big);
+        return {GemmPlan::BIG, 256, big, 4, (int)std::min<long>(resident / 2, tiles), (int)mix};
+    }
+    return {GemmPlan::PERSIST, 128, p192 ? 192 : 128, 8, resident, 0};
+}
+
 template <int EPI>
 void launch_cfg(const GemmArgs& a, hipStream_t s) {
     constexpr int BF = 128, BT = 128;
@@ -1214,47 +1300,20 @@ void launch_cfg(const GemmArgs& a, hipStream_t s) {
         HIP_CHECK(hipGetLastError());
         return;
     }
-    const int resident = resident_tiles();
-    if (a.gather) {
-        JH_LAUNCH((gemm_kernel<EPI, true>), dim3(blocks), dim3(256), 0, s, a);
-    } else if (blocks > resident) {
-        // More tiles than resident workgroups.  Each candidate is costed as its
-        // rounds of resident workgroups times the time one round took on
-        // MI355X (K = 768, N = 2304, one box): persistent 128x128 12.9 us and
-        // 128x192 20.6 us at two workgroups per CU; eight-wave 256x192 19.0
-        // and 256x256 22.4 us at one per CU.
-        auto rounds = [](long tiles, long slots) { return (tiles + slots - 1) / slots; };
-        const long t192 = (long)((a.n + 127) / 128) * ((a.rows + 191) / 192);
-        const long r128 = rounds(blocks, resident), r192 = rounds(t192, resident);
-        // Persistent 128-feature tiles: 192 tokens when their rounds, at 1.5x
-        // the work each, cost no more than the 128-token tiles' rounds.
-        const bool p192 = t192 >= resident && 3 * r192 <= 2 * r128;
-        double best = p192 ? r192 * 20.6 : r128 * 12.9;
-        int big = 0;
-        if (a.n >= 1024) {
-            const int grid = resident / 2;
-            const long nF = (a.n + 255) / 256;
-            // (256x128 never beats the persistent 128x128 tiles: it has at least
-            // their rounds at a higher cost per round.)
-            const int bts[2] = {256, 192};
-            const double per_round[2] = {22.4, 19.0};
-            for (int c = 0; c < 2; ++c) {
-                const double cost = rounds(nF * ((a.rows + bts[c] - 1) / bts[c]), grid) * per_round[c];
-                if (cost < best) best = cost, big = bts[c];
-            }
-        }
-        if (big) {
-            const long tiles = (long)((a.n + 255) / 256) * ((a.rows + big - 1) / big);
-            const dim3 g((unsigned)std::min<long>(resident / 2, tiles));
-            if (big == 256) JH_LAUNCH((gemm_big_kernel<EPI, 256>), g, dim3(512), 0, s, a);
-            else JH_LAUNCH((gemm_big_kernel<EPI, 192>), g, dim3(512), 0, s, a);
-        } else if (p192) {
-            JH_LAUNCH((gemm_persist_kernel<EPI, 192>), dim3(resident), dim3(256), 0, s, a);
-        } else {
-            JH_LAUNCH((gemm_persist_kernel<EPI>), dim3(resident), dim3(256), 0, s, a);
-        }
+    const GemmPlan pl = plan_gemm(a);
+    const dim3 g((unsigned)pl.grid);
+    if (pl.kind == GemmPlan::PLAIN) {
+        if (a.gather) JH_LAUNCH((gemm_kernel<EPI, true>), g, dim3(256), 0, s, a);
+        else JH_LAUNCH((gemm_kernel<EPI, false>), g, dim3(256), 0, s, a);
+    } else if (pl.kind == GemmPlan::BIG) {
+        GemmArgs b = a;
+        b.mix_rows = pl.mix;
+        if (pl.bt == 256) JH_LAUNCH((gemm_big_kernel<EPI, 256>), g, dim3(512), 0, s, b);
+        else JH_LAUNCH((gemm_big_kernel<EPI, 192>), g, dim3(512), 0, s, b);
+    } else if (pl.bt == 192) {
+        JH_LAUNCH((gemm_persist_kernel<EPI, 192>), g, dim3(256), 0, s, a);
     } else {
-        JH_LAUNCH((gemm_kernel<EPI, false>), dim3(blocks), dim3(256), 0, s, a);
+        JH_LAUNCH((gemm_persist_kernel<EPI>), g, dim3(256), 0, s, a);
     }
     HIP_CHECK(hipGetLastError());
 }

@@ -58,6 +58,9 @@ struct GemmArgs {
     const float* ln_w = nullptr;
     const float* ln_b = nullptr;
     float ln_eps = 0.0f;
+    // set by launch_gemm for the eight-wave kernel: rows [0, mix_rows) in
+    // full-height token tiles, the rest in tiles 32 tokens shorter (0: all full)
+    int mix_rows = 0;
 };
 
 void launch_gemm(int epilogue, const GemmArgs& a, hipStream_t stream);

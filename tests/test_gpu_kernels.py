@@ -203,14 +203,19 @@ def test_gemm_192_token_tiles(rows, n, k, epi):
                                           (16500, 1152, 384, abi.EPI_BIAS_RELU_BF16),
                                           (32768, 2304, 768, abi.EPI_STORE_BF16), (32768, 2304, 768, abi.EPI_GEGLU_BF16),
                                           (23000, 1536, 128, abi.EPI_ROPE_BF16), (15000, 1152, 64, abi.EPI_ROPE_BF16),
-                                          (30000, 2304, 64, abi.EPI_GEGLU_BF16)])
+                                          (30000, 2304, 64, abi.EPI_GEGLU_BF16),
+                                          (12000, 2304, 768, abi.EPI_STORE_BF16), (11000, 1536, 768, abi.EPI_ROPE_BF16),
+                                          (24000, 1152, 256, abi.EPI_GEGLU_BF16)])
 def test_gemm_eight_wave_tiles(rows, n, k, epi):
     """Shapes routed to the eight-wave 256-feature GEMM: 256x192 tiles at config1's 9482 tokens, at the Julia-1
     widths (N = 1152 leaves half a 256-feature tile, whose rows past N read as zeros from the buffer range check)
     and with token tiles cut at the end, and 256x256 tiles at 32768 tokens; every epilogue family except the FP32
-    residual (N = 768 stays on the four-wave kernels), against torch FP32.  The last three run one or two K steps
-    per tile with two to four tiles per workgroup, so the next tile's first stage is issued in the tile's first
-    step and the RoPE position/cos/sin prefetch runs in the step that also waits on the previous epilogue."""
+    residual (N = 768 stays on the four-wave kernels), against torch FP32.  The 23000 / 15000 / 30000 shapes run
+    one or two K steps per tile with two to four tiles per workgroup, so the next tile's first stage is issued in
+    the tile's first step and the RoPE position/cos/sin prefetch runs in the step that also waits on the previous
+    epilogue.  Two-phase schedules (a round of full-height tiles, then a round of tiles 32 tokens shorter, whose
+    loader waves multiply one 32-token block fewer): 192/160 at 9482 x 2304, 16500 x 1152, 15000 x 1152 (one K
+    step) and 11000 x 1536; 256/224 at 12000 x 2304 and 24000 x 1152."""
     _check_wide_gemm(rows, n, k, epi, rows + 3 * n + epi)
 
 
