@@ -102,15 +102,22 @@ __global__ __launch_bounds__(256) void final_norm_kernel(float* __restrict__ x, 
     constexpr int H = EPL * 64;
     const int row = xcd_rows_first() + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (row >= rows) return;
-    RowVec<EPL> r, te;
+    // Every load is issued before the first reduction: the token's type row
+    // (behind its tok_meta word), both norms' weights and the row itself, so a
+    // wave waits on one round of memory latency instead of three in a row.
+    const uint32_t qt = (tok_meta[row] >> 16) & 0xff;
+    RowVec<EPL> r, te, g1, g2, b2;
     float* xr = x + (long)row * H;
     r.load(xr, lane);
-    r.layer_norm(fw, nullptr, eps, lane);
-    te.load(type_emb + (long)((tok_meta[row] >> 16) & 0xff) * H, lane);
+    g1.load(fw, lane);
+    g2.load(hw, lane);
+    if (hb) b2.load(hb, lane);
+    te.load(type_emb + (long)qt * H, lane);
+    r.layer_norm(g1, nullptr, eps);
 #pragma unroll
     for (int e = 0; e < EPL; ++e) r.v[e] += te.v[e];
     r.store(xr, lane);
-    r.layer_norm(hw, hb, 1e-5f, lane);
+    r.layer_norm(g2, hb ? &b2 : nullptr, 1e-5f);
     r.store_bf16(out + (long)row * H, lane);
 }
 
