@@ -458,6 +458,24 @@ def test_embed_and_layer_norm(hidden):
     assert np.all(np.abs(host(out) - expect) <= 4e-3 * np.abs(expect) + 1e-5)
 
 
+@pytest.mark.parametrize("rows", [1, 3, 5, 29, 32, 33, 4099])
+def test_layer_norm_covers_every_row(rows):
+    """The row kernels deal their 4-row workgroups to the XCDs in contiguous eighths (workgroup b on XCD b % 8);
+    every row must still be written exactly as the oracle's LayerNorm, for grids of fewer than 8 workgroups, a
+    multiple of 8, and a partial last workgroup (output pre-filled with NaN so a skipped row shows)."""
+    r = rng(100 + rows)
+    hidden = 768
+    xs = r.standard_normal((rows, hidden), dtype=np.float32) * 2 + 0.5
+    w = 1 + 0.1 * r.standard_normal(hidden, dtype=np.float32)
+    b = 0.1 * r.standard_normal(hidden, dtype=np.float32)
+    out = torch.full((rows, hidden), float("nan"), dtype=BF16, device="cuda")
+    hip.op_layer_norm(dev(xs), dev(w), dev(b), 1e-5, out)
+    got = host(out)
+    expect = oracle.layer_norm(xs, w, b, 1e-5)
+    assert np.all(np.isfinite(got))
+    assert np.all(np.abs(got - expect) <= 4e-3 * np.abs(expect) + 1e-5)
+
+
 def test_final_norm_and_scorer():
     r = rng(8)
     rows, hidden = 97, 768
