@@ -527,7 +527,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
 
 // Eight-wave variant for wide outputs (N >= 1024): one workgroup per CU owns
 // a 256-feature x BT-token tile (BT = 192 or 256), eight waves of 64
-// features x BT/2 tokens.  The operand DMA of a K step is 1 KB per
+// features x BT/2 tokens (on a tile 32 tokens shorter, waves 0-3 take 32
+// tokens fewer).  The operand DMA of a K step is 1 KB per
 // instruction through the texture addresser (TA), which drains one
 // instruction per ~16 cycles per CU; a wave blocks while its instructions
 // wait there.  When all waves issue their share right after the step's
