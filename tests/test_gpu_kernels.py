@@ -458,11 +458,12 @@ def test_embed_and_layer_norm(hidden):
     assert np.all(np.abs(host(out) - expect) <= 4e-3 * np.abs(expect) + 1e-5)
 
 
-@pytest.mark.parametrize("rows", [1, 3, 5, 29, 32, 33, 4099])
+@pytest.mark.parametrize("rows", [1, 3, 5, 29, 32, 33, 64, 71, 4096, 4099])
 def test_layer_norm_covers_every_row(rows):
-    """The row kernels deal their 4-row workgroups to the XCDs in contiguous eighths (workgroup b on XCD b % 8);
-    every row must still be written exactly as the oracle's LayerNorm, for grids of fewer than 8 workgroups, a
-    multiple of 8, and a partial last workgroup (output pre-filled with NaN so a skipped row shows)."""
+    """The LayerNorm kernel deals its 8-row workgroups (two rows per wave) to the XCDs in contiguous eighths
+    (workgroup b on XCD b % 8); every row must still be written exactly as the oracle's LayerNorm, for grids of
+    fewer than 8 workgroups, exactly 8 and 512 workgroups, a partial last workgroup, and a wave whose second row
+    is past the end (output pre-filled with NaN so a skipped row shows)."""
     r = rng(100 + rows)
     hidden = 768
     xs = r.standard_normal((rows, hidden), dtype=np.float32) * 2 + 0.5
