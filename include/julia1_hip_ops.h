@@ -99,6 +99,30 @@ int jh_op_gemm_ln(int epilogue, const float* xf, size_t ldx, size_t rows, const 
                   const float* sin_t, size_t rope_cols, const float* ln_w, const float* ln_b, float eps,
                   void* stream);
 
+/*
+ * jh_op_gemm on the weight-stationary kernel: each workgroup (one per CU)
+ * keeps a 256-row slab of W resident (registers and LDS) and streams 16-token
+ * blocks of X through LDS, so only X moves from L2 during the multiply.
+ * w_packed is W (as jh_op_gemm takes it, [n, k] bf16; the GEGLU interleave
+ * for Wi) in the fragment order jh_op_pack_ws writes.  Requires K == 768,
+ * N % 256 == 0, no row gather; epilogues and the other arguments as
+ * jh_op_gemm.  The same bf16 products as jh_op_gemm, summed in FP32 in K
+ * order in steps of 32 (jh_op_gemm: 16), so outputs agree to FP32 rounding.
+ * jh_forward uses it for the K = 768 GEMMs at full batch.  Replaces cuBLAS
+ * gemm_ex (src/cuda/mod.rs:347-375) for those shapes.
+ */
+int jh_op_gemm_ws(int epilogue, const void* x, size_t ldx, size_t rows, const void* w_packed, size_t n,
+                  size_t k, void* out, size_t ldo, size_t col, const float* bias, const int32_t* pos,
+                  const float* cos_t, const float* sin_t, size_t rope_cols, void* stream);
+
+/*
+ * Host: reorder a bf16 W [n, k] (row-major) into jh_op_gemm_ws's fragment
+ * order (n*k elements; n % 256 == 0, k % 32 == 0).  No reference counterpart
+ * (a one-time weight layout, as the reference's BF16 conversion at upload,
+ * src/cuda/mod.rs:36-39).
+ */
+int jh_op_pack_ws(const void* w, size_t n, size_t k, void* out);
+
 /* Reorder a host FP32 Wi [2*inter, k] into the gate/up interleave JH_EPI_GEGLU_BF16 expects. */
 void jh_op_interleave_geglu(const float* wi, size_t inter, size_t k, float* out);
 

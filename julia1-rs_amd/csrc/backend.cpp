@@ -92,14 +92,29 @@ DevBuf upload_bf16(const float* src, size_t n) {
     return upload_bytes(tmp.data(), n * sizeof(bf16_t));
 }
 
+// The same BF16 matrix [n, k] in the weight-stationary GEMM's fragment order
+// (a second copy beside the row-major one, which the other GEMM kernels
+// read), or nothing when that kernel does not take the shape (K != 768 or
+// n % 256 != 0).
+DevBuf upload_bf16_ws(const float* src, size_t n, size_t k) {
+    if (k != 768 || n % 256) return DevBuf();
+    if (!src) throw jh_error(JH_ERR_INVALID, "missing weight tensor");
+    std::vector<bf16_t> tmp(n * k), packed(n * k);
+    for (size_t i = 0; i < n * k; ++i) tmp[i] = f2bf_host(src[i]);
+    pack_ws(tmp.data(), (int)n, (int)k, packed.data());
+    return upload_bytes(packed.data(), n * k * sizeof(bf16_t));
+}
+
 struct EncLayer {
     DevBuf attn_norm, wqkv, wo, mlp_norm, wi, wo2;
+    DevBuf wqkv_ws, wo_ws, wi_ws;  // weight-stationary copies (empty where that kernel does not apply)
     int rope = 0;
     bool global = false;
 };
 
 struct HeadLayer {
     DevBuf norm1_w, norm1_b, in_w, in_b, out_w, out_b, norm2_w, norm2_b, lin1_w, lin1_b, lin2_w, lin2_b;
+    DevBuf in_ws, out_ws, lin1_ws;
 };
 
 constexpr int QTILE = 128;  // queries per attention work item (four waves of 32)
@@ -389,9 +404,10 @@ struct jh_model {
 
     void gemm(int cls, int epi, const void* xp, long ldx, const int32_t* gather, size_t rows, const bf16_t* w, int n,
               int k, void* out, long ldo, int col, const float* bias, const float* cos_t = nullptr,
-              const float* sin_t = nullptr, int rope_cols = 0) {
+              const float* sin_t = nullptr, int rope_cols = 0, const bf16_t* w_ws = nullptr) {
         GemmArgs a{(const bf16_t*)xp, ldx, gather, (int)rows, w, n, k, out, ldo, col, bias,
                    (const int32_t*)d_tok, cos_t, sin_t, rope_cols};
+        a.w_ws = w_ws;
         if (use_splitk) {
             a.partial = splitk.as<float>();
             a.partial_bytes = kSplitkBytes;
@@ -405,7 +421,8 @@ struct jh_model {
     // LayerNorm are one kernel; otherwise the GEMM epilogue adds the residual
     // and a separate LayerNorm follows.
     void gemm_resid_ln(int cls, int ln_cls, const void* xp, long ldx, size_t rows, const bf16_t* w, int k, float* xo,
-                       const float* bias, const float* ln_w, const float* ln_b, float ln_eps, bf16_t* lo) {
+                       const float* bias, const float* ln_w, const float* ln_b, float ln_eps, bf16_t* lo,
+                       const bf16_t* w_ws = nullptr) {
         const int H = h;
         GemmArgs a{(const bf16_t*)xp, ldx, nullptr, (int)rows, w, H, k, xo, H, 0, bias,
                    (const int32_t*)d_tok, nullptr, nullptr, 0};
@@ -416,7 +433,7 @@ struct jh_model {
             S = gemm_splitk_count(JH_EPI_RESID_F32, a);
         }
         if (S <= 1) {
-            gemm(cls, JH_EPI_RESID_F32, xp, ldx, nullptr, rows, w, H, k, xo, H, 0, bias);
+            gemm(cls, JH_EPI_RESID_F32, xp, ldx, nullptr, rows, w, H, k, xo, H, 0, bias, nullptr, nullptr, 0, w_ws);
             layer_norm(ln_cls, xo, rows, ln_w, ln_b, ln_eps, lo);
             return;
         }
@@ -517,7 +534,7 @@ struct jh_model {
                 layer_norm(K_LN, x.as<float>(), t, L.attn_norm.as<float>(), nullptr, eps, xn.as<bf16_t>());
             xn_ready = false;
             gemm(K_QKV, JH_EPI_ROPE_BF16, xn.p, H, nullptr, t, L.wqkv.as<bf16_t>(), 3 * H, H, qkv.p, 3 * H, 0, nullptr,
-                 ropes[L.rope].first.as<float>(), ropes[L.rope].second.as<float>(), 2 * H);
+                 ropes[L.rope].first.as<float>(), ropes[L.rope].second.as<float>(), 2 * H, L.wqkv_ws.as<bf16_t>());
             const bf16_t* q = qkv.as<bf16_t>();
             if (L.global)
                 attention(K_ATTN_GLOBAL, q, 3 * H, q + H, q + 2 * H, 3 * H, ctx.as<bf16_t>(), H, d_tiles, ntiles, heads,
@@ -526,9 +543,9 @@ struct jh_model {
                 attention(K_ATTN_LOCAL, q, 3 * H, q + H, q + 2 * H, 3 * H, ctx.as<bf16_t>(), H, d_tiles, ntiles, heads,
                           half_window, pairs_local, (double)t);
             gemm_resid_ln(K_WO, K_LN, ctx.p, H, t, L.wo.as<bf16_t>(), H, x.as<float>(), nullptr,
-                          L.mlp_norm.as<float>(), nullptr, eps, xn.as<bf16_t>());
+                          L.mlp_norm.as<float>(), nullptr, eps, xn.as<bf16_t>(), L.wo_ws.as<bf16_t>());
             gemm(K_WI, JH_EPI_GEGLU_BF16, xn.p, H, nullptr, t, L.wi.as<bf16_t>(), 2 * inter, H, hbuf.p, inter, 0,
-                 nullptr);
+                 nullptr, nullptr, nullptr, 0, L.wi_ws.as<bf16_t>());
             if (l + 1 < upto && layers[l + 1].attn_norm.p) {
                 gemm_resid_ln(K_WO2, K_LN, hbuf.p, inter, t, L.wo2.as<bf16_t>(), inter, x.as<float>(), nullptr,
                               layers[l + 1].attn_norm.as<float>(), nullptr, eps, xn.as<bf16_t>());
@@ -554,22 +571,25 @@ struct jh_model {
         for (int j = 0; j + 1 < nh; ++j) {
             HeadLayer& L = head[j];
             gemm(K_HEAD_GEMM, JH_EPI_BIAS_BF16, xn.p, H, nullptr, t, L.in_w.as<bf16_t>(), 3 * H, H, qkv.p, 3 * H, 0,
-                 L.in_b.as<float>());
+                 L.in_b.as<float>(), nullptr, nullptr, 0, L.in_ws.as<bf16_t>());
             const bf16_t* q = qkv.as<bf16_t>();
             attention(K_HEAD_ATTN, q, 3 * H, q + H, q + 2 * H, 3 * H, ctx.as<bf16_t>(), H, d_tiles, ntiles, head_heads,
                       -1, pairs_global, (double)t);
             gemm_resid_ln(K_HEAD_GEMM, K_HEAD_ROWS, ctx.p, H, t, L.out_w.as<bf16_t>(), H, x.as<float>(),
-                          L.out_b.as<float>(), L.norm2_w.as<float>(), L.norm2_b.as<float>(), 1e-5f, xn.as<bf16_t>());
+                          L.out_b.as<float>(), L.norm2_w.as<float>(), L.norm2_b.as<float>(), 1e-5f, xn.as<bf16_t>(),
+                          L.out_ws.as<bf16_t>());
             gemm(K_HEAD_GEMM, JH_EPI_BIAS_RELU_BF16, xn.p, H, nullptr, t, L.lin1_w.as<bf16_t>(), ff, H, hbuf.p, ff, 0,
-                 L.lin1_b.as<float>());
+                 L.lin1_b.as<float>(), nullptr, nullptr, 0, L.lin1_ws.as<bf16_t>());
             HeadLayer& N = head[j + 1];
             gemm_resid_ln(K_HEAD_GEMM, K_HEAD_ROWS, hbuf.p, ff, t, L.lin2_w.as<bf16_t>(), ff, x.as<float>(),
                           L.lin2_b.as<float>(), N.norm1_w.as<float>(), N.norm1_b.as<float>(), 1e-5f, xn.as<bf16_t>());
         }
         HeadLayer& L = head[nh - 1];
         // Keys/values for every token: in_proj rows [H, 3H) into qkv columns [H, 3H).
+        // (In the weight-stationary copy, 256-row slabs are contiguous, so rows [H, 3H) start H·H elements in.)
         gemm(K_HEAD_GEMM, JH_EPI_BIAS_BF16, xn.p, H, nullptr, t, L.in_w.as<bf16_t>() + (size_t)H * H, 2 * H, H, qkv.p,
-             3 * H, H, L.in_b.as<float>() + H);
+             3 * H, H, L.in_b.as<float>() + H, nullptr, nullptr, 0,
+             L.in_ws.p && H % 256 == 0 ? L.in_ws.as<bf16_t>() + (size_t)H * H : nullptr);
         // Queries for markers only, gathered straight from the normed rows.
         gemm(K_HEAD_GEMM, JH_EPI_BIAS_BF16, xn.p, H, d_markers, m, L.in_w.as<bf16_t>(), H, H, qm.p, H, 0,
              L.in_b.as<float>());
@@ -743,11 +763,14 @@ void build_model(jh_model* m, const jh_config* c, const jh_weights* w, int ordin
         if (l > 0 && !s.attn_norm) throw jh_error(JH_ERR_INVALID, "encoder layers after the first need attn_norm");
         if (s.attn_norm) L.attn_norm = upload_f32(s.attn_norm, H);
         L.wqkv = upload_bf16(s.wqkv, 3 * H * H);
+        L.wqkv_ws = upload_bf16_ws(s.wqkv, 3 * H, H);
         L.wo = upload_bf16(s.wo, H * H);
+        L.wo_ws = upload_bf16_ws(s.wo, H, H);
         L.mlp_norm = upload_f32(s.mlp_norm, H);
         if (!s.wi) throw jh_error(JH_ERR_INVALID, "missing Wi");
         jh_op_interleave_geglu(s.wi, I, H, wi_tmp.data());
         L.wi = upload_bf16(wi_tmp.data(), 2 * I * H);
+        L.wi_ws = upload_bf16_ws(wi_tmp.data(), 2 * I, H);
         L.wo2 = upload_bf16(s.wo2, H * I);
         L.global = c->global[l] != 0;
         const float th = c->rope_theta[l];
@@ -771,8 +794,11 @@ void build_model(jh_model* m, const jh_config* c, const jh_weights* w, int ordin
         L.norm1_w = upload_f32(s.norm1_w, H); L.norm1_b = upload_f32(s.norm1_b, H);
         L.in_w = upload_bf16(s.in_w, 3 * H * H); L.in_b = upload_f32(s.in_b, 3 * H);
         L.out_w = upload_bf16(s.out_w, H * H); L.out_b = upload_f32(s.out_b, H);
+        L.in_ws = upload_bf16_ws(s.in_w, 3 * H, H);
+        L.out_ws = upload_bf16_ws(s.out_w, H, H);
         L.norm2_w = upload_f32(s.norm2_w, H); L.norm2_b = upload_f32(s.norm2_b, H);
         L.lin1_w = upload_bf16(s.lin1_w, F * H); L.lin1_b = upload_f32(s.lin1_b, F);
+        L.lin1_ws = upload_bf16_ws(s.lin1_w, F, H);
         L.lin2_w = upload_bf16(s.lin2_w, H * F); L.lin2_b = upload_f32(s.lin2_b, H);
         m->head.push_back(std::move(L));
     }

@@ -1301,6 +1301,12 @@ void launch_cfg(const GemmArgs& a, hipStream_t s) {
         HIP_CHECK(hipGetLastError());
         return;
     }
+    // Weight-stationary kernel when W comes packed for it and each token
+    // range gets at least 64 tokens (its 384 KB W slab per CU is read once).
+    if (gemm_ws_supported(EPI, a) && a.rows >= 64 * gemm_ws_ranges(a)) {
+        launch_gemm_ws(EPI, a, s);
+        return;
+    }
     const GemmPlan pl = plan_gemm(a);
     const dim3 g((unsigned)pl.grid);
     if (pl.kind == GemmPlan::PLAIN) {
@@ -1356,6 +1362,8 @@ bool validate_gemm(int epi, const GemmArgs& a) {
 }
 
 }  // namespace
+
+bool validate_gemm_args(int epi, const GemmArgs& a) { return validate_gemm(epi, a); }
 
 int gemm_splitk_count(int epi, const GemmArgs& a) {
     if (!validate_gemm(epi, a)) return 1;

@@ -1,0 +1,440 @@
+// Weight-stationary BF16 GEMM for gfx950 at K = 768 (the encoder's Wqkv, Wi
+// and Wo, and the head's K = 768 projections at full batch).
+//
+// out = epi(X · Wᵀ) as in gemm.hip, but each workgroup keeps a 256-row slab
+// of W resident for its whole life (160 VGPRs per lane and 64 KB of LDS) and
+// streams only X through LDS.  One workgroup per CU, eight waves (two per
+// SIMD); wave w owns 32 W rows as two 16-row blocks ("lo" and "hi") × 768 K,
+// i.e. 48 A-fragments of v_mfma_f32_16x16x32_bf16, and multiplies them with
+// each 16-token X block that lands in LDS: 48 MFMAs per block and wave in two
+// independent accumulator chains, each summing K in order.
+//
+// Why: at K = 768 the tiled kernels are bound by moving both operands from L2
+// into LDS (a 256×192 tile needs ~37 B/clk per CU at full MFMA rate and gets
+// ~27).  Here only X moves in the loop: each X element is used for 256 W rows,
+// 16 B/clk per CU at full MFMA rate, plus the one-time 384 KB W slab per CU.
+//
+// Layout.  W comes pre-packed (jh_op_pack_ws) so that each wave's fragment
+// (slice s, block lo/hi) is one contiguous 1 KB block in A-fragment order
+// (lane l: W row l % 16 of the block, K 32s + 8(l/16) .. +8): coalesced
+// 16-byte loads.  The slab's 256 rows are the 64-row blocks 4f .. 4f+3 of W;
+// wave w takes rows x0 .. x0+15 (lo) and 32+x0 .. 32+x0+15 (hi) of block
+// 4f + w/2 (x0 = 16 (w % 2)).  In the 16×16 accumulator layout (lane l: token
+// l % 16, rows 4(l/16) .. +3) each lane then holds the RoPE pair (d, d+32) and
+// the GEGLU pair (gate, up) of gemm.hip's interleaved Wi in lo[i] and hi[i].
+// An X block is 16 tokens × 768 K in 12 stages of [16 rows][128 B], 16-byte
+// chunks XOR-swizzled by (row >> 1) & 7 as in gemm.hip (conflict-free B-fragment
+// reads).  RoPE cos/sin rows of the block's tokens are gathered into LDS by DMA.
+//
+// Schedule.  Workgroups are (token range, feature slab) pairs, dealt so that
+// the slabs sharing a token range sit on one XCD (X read once per L2).  Per
+// 16-token block: one barrier; then every wave runs the block's 48 MFMAs and,
+// between them, issues its share of the next block's X DMA (into the other of
+// two X slots) and runs the previous block's epilogue from its second set of
+// accumulators, so the epilogue's VALU work and stores issue under the MFMAs
+// and both waves of a SIMD stay in their MFMA stream.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <type_traits>
+
+#include "../../include/julia1_hip_ops.h"
+#include "kernels.hpp"
+
+namespace {
+
+constexpr int WS_K = 768;
+constexpr int WS_S = WS_K / 32;          // 32-deep K slices
+constexpr int WS_SL = 4;                 // the last WS_SL slices' fragments stay in LDS (registers are the limit)
+constexpr int WS_SR = WS_S - WS_SL;      // slices whose fragments are held in VGPRs
+constexpr int WS_ROWS = 256;             // W rows per workgroup
+constexpr int WS_TB = 16;                // tokens per block
+constexpr int WS_XSLOT = WS_TB * WS_K;   // bf16 elements per X slot (24 KB)
+constexpr int WS_NCS = 3;                // cos/sin and position slots (RoPE)
+constexpr int WS_CSLOT = WS_TB * 32;     // floats per cos (or sin) slot
+constexpr int WS_PD = 6;                 // B-fragment reads in flight
+
+__device__ constexpr int swz(int r) { return (r >> 1) & 7; }
+
+// rotate-half RoPE of one (d, d+32) pair, as gemm.hip's epilogue writes it
+__device__ inline void rope_pair(float& lo, float& hi, float c, float s) {
+    const float x0 = lo, x1 = hi;
+    lo = x0 * c - x1 * s;
+    hi = x1 * c + x0 * s;
+}
+
+template <int EPI>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void gemm_ws_kernel(GemmArgs a, int nF,
+                                                                                               int R, int nTB) {
+    constexpr bool ROPE = EPI == JH_EPI_ROPE_BF16;
+    constexpr bool GEGLU = EPI == JH_EPI_GEGLU_BF16;
+    constexpr bool F32OUT = EPI == JH_EPI_RESID_F32 || EPI == JH_EPI_BIAS_F32;
+    constexpr bool BIASED = EPI == JH_EPI_BIAS_BF16 || EPI == JH_EPI_BIAS_RELU_BF16 || EPI == JH_EPI_BIAS_F32;
+    __shared__ __align__(1024) bf16_t sx[2 * WS_XSLOT];
+    __shared__ __align__(1024) bf16_t swl[8 * WS_SL * 2 * 512];  // each wave's LDS-held fragments
+    __shared__ __align__(16) float scs[ROPE ? WS_NCS * 2 * WS_CSLOT : 4];
+    __shared__ __align__(16) int spos[ROPE ? WS_NCS * 64 : 4];   // token metadata of a block, DMA'd
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // Workgroup -> (token range r, slab f): consecutive ids u share r, and an
+    // XCD (workgroup b runs on XCD b % 8) gets a contiguous run of u.
+    const int G = gridDim.x, bid = blockIdx.x;
+    const int xcd = bid & 7, local = bid >> 3, q8 = G >> 3, r8 = G & 7;
+    const int u = xcd * q8 + (xcd < r8 ? xcd : r8) + local;
+    const int r = u / nF, f = u - r * nF;
+    const int b0 = (int)((long)r * nTB / R), b1 = (int)((long)(r + 1) * nTB / R);
+    if (b0 >= b1) return;
+
+    // X DMA: instruction i of a block (0..23) fills stage i/2, rows
+    // 8(i%2) .. +7; wave w issues i = w, w+8, w+16 (one row half), lane j row
+    // 8(w%2) + j/8, the 16-byte chunk that belongs in slot j % 8.  Blocks past
+    // the range get an empty resource: their loads read zeros into a slot
+    // nothing reads, which keeps the issue branch-free.
+    const int drow = 8 * (wave & 1) + (lane >> 3);
+    const uint32_t dchunk = (uint32_t)(((lane & 7) ^ swz(drow)) * 16);
+    const uint32_t xoff = (uint32_t)drow * (uint32_t)a.ldx * 2 + dchunk;
+    auto x_rsrc = [&](int bb) {
+        const int t0 = bb * WS_TB;
+        return bb < b1 ? make_rsrc(a.x + (long)t0 * a.ldx, (uint64_t)(a.rows - 1 - t0) * a.ldx * 2 + (uint64_t)WS_K * 2)
+                       : make_rsrc(a.x, 0);
+    };
+    auto issue_x = [&](const i32x4& rx, int slot, int j) {  // j-th of this wave's three
+        const int i = wave + 8 * j;
+        const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+            (uint32_t)(uintptr_t)&sx[slot * WS_XSLOT + (i >> 1) * 1024 + (i & 1) * 512]);
+        asm volatile("buffer_load_dwordx4 %1, %2, %3 offen lds" ::"{m0}"(m0), "v"(xoff), "s"(rx), "s"((i >> 1) * 128)
+                     : "memory");
+    };
+    // RoPE: the cos and sin rows of the block's tokens, row i at [i][32]
+    // (16-byte chunks swizzled as the X rows), at the positions that
+    // issue_pos brought into LDS a block earlier.  (Positions go through LDS
+    // because a register load would make the compiler wait for it, and vmcnt
+    // completes in order: that wait would also wait for every DMA and W load
+    // issued before it.)  Waves 0-3 issue one instruction each (cos or sin,
+    // rows 0-7 or 8-15); only slabs with rotated rows need the tables.
+    const bool rot_slab = ROPE && WS_ROWS * f < a.rope_cols;
+    auto issue_pos = [&](int bb, int slot) {  // wave 0: tok_meta of tokens bb·16 .. (64 lanes)
+        if constexpr (ROPE) {
+            if (rot_slab && wave == 0) {
+                const int t0 = bb * WS_TB;
+                const i32x4 rp = bb < b1 ? make_rsrc(a.pos + t0, (uint64_t)(a.rows - t0) * 4) : make_rsrc(a.pos, 0);
+                const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&spos[slot * 64]);
+                asm volatile("buffer_load_dword %1, %2, %3 offen lds" ::"{m0}"(m0), "v"((uint32_t)lane * 4),
+                             "s"(rp), "s"(0)
+                             : "memory");
+            }
+        }
+    };
+    auto issue_cs = [&](int bb, int slot) {
+        if constexpr (ROPE) {
+            if (rot_slab && wave < 4) {
+                const int p = spos[slot * 64 + drow] & 0xffff;
+                const float* tab = (wave & 2) ? a.sin_t : a.cos_t;
+                const i32x4 rt = make_rsrc(tab, bb < b1 ? 65536ull * 128 : 0);
+                const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+                    (uint32_t)(uintptr_t)&scs[(2 * slot + (wave >> 1)) * WS_CSLOT + (wave & 1) * 256]);
+                asm volatile("buffer_load_dwordx4 %1, %2, %3 offen lds" ::"{m0}"(m0), "v"((uint32_t)p * 128 + dchunk),
+                             "s"(rt), "s"(0)
+                             : "memory");
+            }
+        }
+    };
+
+    // Prologue.  The first block's X (and the positions of the first two
+    // blocks) ahead of every W load in the CU's queue; then every wave's W
+    // fragments: slices 0 .. WS_SR-1 into VGPRs (in K order, pinned: the
+    // scheduler otherwise reorders them and the first MFMA waits for nearly
+    // all of them; they land in order and the first block's MFMAs wait for
+    // each in turn), the rest by DMA into this wave's LDS fragments.
+    const bool two = b0 + 1 < b1;
+    {
+        const i32x4 rx = x_rsrc(b0);
+#pragma unroll
+        for (int j = 0; j < 3; ++j) issue_x(rx, 0, j);
+        issue_pos(b0, 0);
+        if (two) issue_pos(b0 + 1, 1);
+    }
+    __syncthreads();
+    bf16x8 wf[WS_SR][2];
+    const bf16_t* wp = a.w_ws + (long)(f * 8 + wave) * WS_S * 2 * 512;
+#pragma unroll
+    for (int s = 0; s < WS_SR; ++s)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            wf[s][h] = *(const bf16x8*)(wp + (s * 2 + h) * 512 + lane * 8);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    {
+        const i32x4 rw = make_rsrc(wp + WS_SR * 2 * 512, WS_SL * 2 * 1024);
+#pragma unroll
+        for (int j = 0; j < WS_SL * 2; ++j) {
+            const uint32_t m0 =
+                __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&swl[(wave * WS_SL * 2 + j) * 512]);
+            asm volatile("buffer_load_dwordx4 %1, %2, %3 offen lds" ::"{m0}"(m0), "v"((uint32_t)lane * 16), "s"(rw),
+                         "s"(j * 1024)
+                         : "memory");
+        }
+    }
+    // the first block's X and positions landed (48 W loads and DMAs since)
+    asm volatile("s_waitcnt vmcnt(48)" ::: "memory");
+    __syncthreads();
+
+    const int tk = lane & 15, kg = lane >> 4;  // B-fragment token, K group; accumulator rows 4·kg ..
+    const int hb = 4 * f + (wave >> 1), x0 = 16 * (wave & 1);
+    const bf16_t* WL = swl + wave * WS_SL * 2 * 512 + lane * 8;
+    f32x4 acc[2][2];  // [set][lo/hi]
+
+    // Epilogue of block bb from accumulator set P: lane (tk, kg) holds token
+    // bb·16 + tk, columns x0 + 4kg .. +3 of the lo half (acc[P][0]) and of the
+    // hi half (acc[P][1]).  Split into steps so the block loop can spread
+    // them between its MFMAs.  Lanes l, l+16, l+32, l+48 write one token's 32
+    // contiguous bytes per half.
+    struct EpiState {
+        f32x4 lo, hi, c, sn;
+        int t;
+    };
+    auto epi_begin = [&](EpiState& e, int P, int bb) {
+        e.t = bb * WS_TB + tk;
+        e.lo = acc[P][0];
+        e.hi = acc[P][1];
+    };
+    // Step j (0..4) of the elementwise part: j = 0 loads what the others
+    // need (cos/sin rows from LDS, bias), j = 1..4 finish column i = j - 1,
+    // so the VALU work spreads over five MFMA slices.
+    auto epi_step = [&](EpiState& e, int j, int cslot) {
+        if constexpr (ROPE) {
+            if (hb * 64 < a.rope_cols) {
+                if (j == 0) {
+                    const float* C = scs + (2 * cslot) * WS_CSLOT;
+                    const float* S = C + WS_CSLOT;
+                    const int ch = (((x0 >> 2) + kg) ^ swz(tk)) * 4;
+                    e.c = *(const f32x4*)&C[tk * 32 + ch];
+                    e.sn = *(const f32x4*)&S[tk * 32 + ch];
+                } else {
+                    float l = e.lo[j - 1], h = e.hi[j - 1];
+                    rope_pair(l, h, e.c[j - 1], e.sn[j - 1]);
+                    e.lo[j - 1] = l;
+                    e.hi[j - 1] = h;
+                }
+            }
+        }
+        if constexpr (GEGLU) {
+            if (j > 0) e.lo[j - 1] = gelu_erf(e.lo[j - 1]) * e.hi[j - 1];
+        }
+        if constexpr (BIASED) {
+            if (j == 0) {
+                e.c = *(const f32x4*)(a.bias + 64 * hb + x0 + 4 * kg);
+                e.sn = *(const f32x4*)(a.bias + 64 * hb + 32 + x0 + 4 * kg);
+            } else {
+                e.lo[j - 1] += e.c[j - 1];
+                e.hi[j - 1] += e.sn[j - 1];
+                if constexpr (EPI == JH_EPI_BIAS_RELU_BF16) {
+                    e.lo[j - 1] = fmaxf(e.lo[j - 1], 0.0f);
+                    e.hi[j - 1] = fmaxf(e.hi[j - 1], 0.0f);
+                }
+            }
+        }
+    };
+    auto epi_math = [&](EpiState& e, int cslot) {
+#pragma unroll
+        for (int j = 0; j < 5; ++j) epi_step(e, j, cslot);
+    };
+    auto epi_store = [&](EpiState& e) {
+        if (e.t >= a.rows) return;
+        if constexpr (GEGLU) {
+            *(u32x2*)((bf16_t*)a.out + (long)e.t * a.ldo + a.col + 32 * hb + x0 + 4 * kg) =
+                u32x2{pack2(e.lo[0], e.lo[1]), pack2(e.lo[2], e.lo[3])};
+        } else if constexpr (F32OUT) {
+            float* o = (float*)a.out + (long)e.t * a.ldo + a.col + 64 * hb + x0 + 4 * kg;
+            if constexpr (EPI == JH_EPI_RESID_F32) {
+                const f32x4 olo = *(const f32x4*)o, ohi = *(const f32x4*)(o + 32);
+                f32x4 lo = e.lo, hi = e.hi;
+                if (a.bias) {
+                    const f32x4 b_lo = *(const f32x4*)(a.bias + 64 * hb + x0 + 4 * kg);
+                    const f32x4 b_hi = *(const f32x4*)(a.bias + 64 * hb + 32 + x0 + 4 * kg);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        lo[i] += b_lo[i];
+                        hi[i] += b_hi[i];
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    lo[i] = olo[i] + lo[i];
+                    hi[i] = ohi[i] + hi[i];
+                }
+                *(f32x4*)o = lo;
+                *(f32x4*)(o + 32) = hi;
+            } else {
+                *(f32x4*)o = e.lo;
+                *(f32x4*)(o + 32) = e.hi;
+            }
+        } else {
+            bf16_t* o = (bf16_t*)a.out + (long)e.t * a.ldo + a.col + 64 * hb + x0 + 4 * kg;
+            *(u32x2*)o = u32x2{pack2(e.lo[0], e.lo[1]), pack2(e.lo[2], e.lo[3])};
+            *(u32x2*)(o + 32) = u32x2{pack2(e.hi[0], e.hi[1]), pack2(e.hi[2], e.hi[3])};
+        }
+    };
+
+    // One block bb into accumulator set P from X slot (bb - b0) % 2.  Between
+    // the MFMAs: the next block's X DMA (after slices 1, 3, 5), its RoPE rows
+    // (7) and the positions of the block after (9), and, with EPI_PREV, the
+    // previous block's epilogue from set 1-P (elementwise steps after slices
+    // 10-14, stores after 16: the last VMEM instructions of the block).  FIRST: block b0,
+    // whose W fragments are still landing (the compiler waits for each before
+    // its MFMA) and whose LDS-held fragments must have landed before they are
+    // read; it also gathers its own RoPE rows.
+    auto block = [&](auto PC, auto EPI_PREV, auto FIRST, int bb) {
+        constexpr int P = decltype(PC)::value;
+        const int k = bb - b0;
+        const bf16_t* X = sx + (k & 1) * WS_XSLOT;
+        auto rd = [&](int s) {
+            const int c = (s & 1) * 4 + kg;
+            return *(const bf16x8*)&X[(s >> 1) * 1024 + tk * 64 + ((c ^ swz(tk)) * 8)];
+        };
+        const i32x4 rx = x_rsrc(bb + 1);
+        EpiState e;
+        if constexpr (decltype(EPI_PREV)::value) epi_begin(e, 1 - P, bb - 1);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) acc[P][h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        bf16x8 bx[WS_PD], wl[2][2];
+#pragma unroll
+        for (int p = 0; p < WS_PD; ++p) bx[p] = rd(p);
+#pragma unroll
+        for (int s = 0; s < WS_S; ++s) {
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const bf16x8 w = s < WS_SR ? wf[s < WS_SR ? s : 0][h] : wl[(s - WS_SR) & 1][h];
+                acc[P][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w, bx[s % WS_PD], acc[P][h], 0, 0, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            if (s + WS_PD < WS_S) bx[s % WS_PD] = rd(s + WS_PD);
+            if (s >= WS_SR - 2 && s < WS_S - 2) {  // LDS-held fragments of slice s + 2 (two buffers)
+                if (decltype(FIRST)::value && s == WS_SR - 2) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                const int sl = s + 2 - WS_SR;
+#pragma unroll
+                for (int h = 0; h < 2; ++h) wl[sl & 1][h] = *(const bf16x8*)&WL[(sl * 2 + h) * 512];
+            }
+            if (s == 1 || s == 3 || s == 5) issue_x(rx, (k + 1) & 1, s >> 1);
+            if (s == 7) {
+                if (decltype(FIRST)::value) issue_cs(b0, 0);
+                issue_cs(bb + 1, (k + 1) % WS_NCS);
+            }
+            if (s == 9) issue_pos(bb + 2, (k + 2) % WS_NCS);
+            if constexpr (decltype(EPI_PREV)::value) {
+                if (s >= 10 && s < 15) epi_step(e, s - 10, (k - 1) % WS_NCS);
+                if (s == 16) epi_store(e);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    using C0 = std::integral_constant<int, 0>;
+    using C1 = std::integral_constant<int, 1>;
+    using T = std::true_type;
+    using F = std::false_type;
+
+    // Each block starts with a barrier (its X, RoPE rows and positions
+    // landed; the slots of two blocks back are free), for which each wave
+    // waits for its own DMA, but not for the stores of the epilogue it ran
+    // since: those are its last VMEM instructions, at least 2 of them (1 for
+    // GEGLU; issued since every block has a live token).
+    auto sync = [&](int k) {
+        if (k == 1) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        else if constexpr (GEGLU) asm volatile("s_waitcnt vmcnt(1)" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+        __syncthreads();
+    };
+    block(C0{}, F{}, T{}, b0);
+    int bb = b0 + 1;
+    for (; bb + 1 < b1; bb += 2) {
+        sync(bb - b0);
+        block(C1{}, T{}, F{}, bb);
+        sync(bb + 1 - b0);
+        block(C0{}, T{}, F{}, bb + 1);
+    }
+    if (bb < b1) {
+        sync(bb - b0);
+        block(C1{}, T{}, F{}, bb);
+    }
+    // The last block's epilogue (its RoPE rows landed at its own barrier,
+    // except for a single-block range, whose rows were issued in its block).
+    if (b1 == b0 + 1) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+    }
+    EpiState e;
+    const int kl = b1 - 1 - b0;
+    if (kl & 1) epi_begin(e, 1, b1 - 1);
+    else epi_begin(e, 0, b1 - 1);
+    epi_math(e, kl % WS_NCS);
+    epi_store(e);
+}
+
+int device_cus() {
+    static std::atomic<int> cached[64];
+    int dev = 0;
+    HIP_CHECK(hipGetDevice(&dev));
+    if (dev < 0 || dev >= 64) throw jh_error(1, "gemm: device ordinal out of range");
+    int v = cached[dev].load(std::memory_order_relaxed);
+    if (v == 0) {
+        HIP_CHECK(hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev));
+        v = std::max(v, 1);
+        cached[dev].store(v, std::memory_order_relaxed);
+    }
+    return v;
+}
+
+}  // namespace
+
+bool gemm_ws_supported(int epi, const GemmArgs& a) {
+    return a.w_ws && a.k == WS_K && a.n % WS_ROWS == 0 && !a.gather && !a.xf && a.rows > 0 &&
+           ((uintptr_t)a.w_ws & 15) == 0 && epi >= JH_EPI_STORE_BF16 && epi <= JH_EPI_BIAS_F32;
+}
+
+// Token ranges per slab: as many as fill the CUs (at most one block each).
+int gemm_ws_ranges(const GemmArgs& a) {
+    const int nF = a.n / WS_ROWS, nTB = (a.rows + WS_TB - 1) / WS_TB;
+    return std::max(1, std::min(nTB, device_cus() / nF));
+}
+
+int gemm_ws_block_tokens() { return WS_TB; }
+
+void launch_gemm_ws(int epi, const GemmArgs& a, hipStream_t s) {
+    if (!gemm_ws_supported(epi, a)) throw jh_error(1, "gemm: weight-stationary kernel needs packed W, K = 768, N % 256 == 0");
+    const int nF = a.n / WS_ROWS, nTB = (a.rows + WS_TB - 1) / WS_TB, R = gemm_ws_ranges(a);
+    const dim3 grid((unsigned)(nF * R)), block(512);
+    switch (epi) {
+        case JH_EPI_STORE_BF16: JH_LAUNCH((gemm_ws_kernel<JH_EPI_STORE_BF16>), grid, block, 0, s, a, nF, R, nTB); break;
+        case JH_EPI_ROPE_BF16: JH_LAUNCH((gemm_ws_kernel<JH_EPI_ROPE_BF16>), grid, block, 0, s, a, nF, R, nTB); break;
+        case JH_EPI_GEGLU_BF16: JH_LAUNCH((gemm_ws_kernel<JH_EPI_GEGLU_BF16>), grid, block, 0, s, a, nF, R, nTB); break;
+        case JH_EPI_RESID_F32: JH_LAUNCH((gemm_ws_kernel<JH_EPI_RESID_F32>), grid, block, 0, s, a, nF, R, nTB); break;
+        case JH_EPI_BIAS_BF16: JH_LAUNCH((gemm_ws_kernel<JH_EPI_BIAS_BF16>), grid, block, 0, s, a, nF, R, nTB); break;
+        case JH_EPI_BIAS_RELU_BF16:
+            JH_LAUNCH((gemm_ws_kernel<JH_EPI_BIAS_RELU_BF16>), grid, block, 0, s, a, nF, R, nTB);
+            break;
+        case JH_EPI_BIAS_F32: JH_LAUNCH((gemm_ws_kernel<JH_EPI_BIAS_F32>), grid, block, 0, s, a, nF, R, nTB); break;
+        default: throw jh_error(1, "gemm: unknown epilogue");
+    }
+    HIP_CHECK(hipGetLastError());
+}
+
+// Host-side packing of a bf16 [n, k] row-major W into the weight-stationary
+// fragment order: [slab f][wave w][slice s][lo/hi h][lane l][8], lane l
+// holding W row 64(4f + w/2) + 32h + 16(w % 2) + l % 16, K 32s + 8(l/16) .. +8.
+void pack_ws(const bf16_t* w, int n, int k, bf16_t* out) {
+    const int ns = k / 32;
+    for (int f = 0; f < n / WS_ROWS; ++f)
+        for (int wave = 0; wave < 8; ++wave)
+            for (int s = 0; s < ns; ++s)
+                for (int h = 0; h < 2; ++h)
+                    for (int lane = 0; lane < 64; ++lane) {
+                        const int rw = 64 * (4 * f + wave / 2) + 32 * h + 16 * (wave % 2) + lane % 16;
+                        bf16_t* o = out + (((((long)f * 8 + wave) * ns + s) * 2 + h) * 64 + lane) * 8;
+                        const bf16_t* src = w + (long)rw * k + 32 * s + 8 * (lane / 16);
+                        for (int e = 0; e < 8; ++e) o[e] = src[e];
+                    }
+}

@@ -61,6 +61,8 @@ struct GemmArgs {
     // set by launch_gemm for the eight-wave kernel: rows [0, mix_rows) in
     // full-height token tiles, the rest in tiles 32 tokens shorter (0: all full)
     int mix_rows = 0;
+    // W pre-packed for the weight-stationary kernel (pack_ws), or null
+    const bf16_t* w_ws = nullptr;
 };
 
 void launch_gemm(int epilogue, const GemmArgs& a, hipStream_t stream);
@@ -72,6 +74,17 @@ int gemm_splitk_count(int epilogue, const GemmArgs& a);
 // only kernel with the LayerNorm prologue); false for rows == 0.
 bool gemm_uses_small(int epilogue, const GemmArgs& a);
 void launch_gemm_partial(int epilogue, const GemmArgs& a, int splits, hipStream_t stream);
+// Weight-stationary kernel (gemm_ws.hip): K = 768, N % 256 == 0, a.w_ws set,
+// no gather or LayerNorm prologue.  gemm_ws_ranges is the number of token
+// ranges each 256-row slab is split into (one workgroup per CU).
+bool gemm_ws_supported(int epilogue, const GemmArgs& a);
+// The shape, alignment and argument checks of launch_gemm (throws jh_error);
+// false when there is nothing to do (rows == 0).
+bool validate_gemm_args(int epilogue, const GemmArgs& a);
+int gemm_ws_ranges(const GemmArgs& a);
+int gemm_ws_block_tokens();
+void launch_gemm_ws(int epilogue, const GemmArgs& a, hipStream_t stream);
+void pack_ws(const bf16_t* w, int n, int k, bf16_t* out);
 
 struct AttnTile {
     int32_t q_row, nq, kv_row, kv_len, q_pos;

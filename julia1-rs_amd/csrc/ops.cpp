@@ -60,6 +60,30 @@ int jh_op_gemm_ln(int epilogue, const float* xf, size_t ldx, size_t rows, const 
     });
 }
 
+int jh_op_gemm_ws(int epilogue, const void* x, size_t ldx, size_t rows, const void* w_packed, size_t n, size_t k,
+                  void* out, size_t ldo, size_t col, const float* bias, const int32_t* pos, const float* cos_t,
+                  const float* sin_t, size_t rope_cols, void* stream) {
+    return jh_guarded([&] {
+        GemmArgs a{(const bf16_t*)x, (long)ldx, nullptr, as_int(rows, "rows"), (const bf16_t*)w_packed,
+                   as_int(n, "n"), as_int(k, "k"), out, (long)ldo, as_int(col, "col"), bias, pos, cos_t, sin_t,
+                   as_int(rope_cols, "rope_cols")};
+        a.w_ws = (const bf16_t*)w_packed;
+        if (!gemm_ws_supported(epilogue, a))
+            throw jh_error(1, "gemm: weight-stationary kernel needs packed W, K = 768, N % 256 == 0");
+        if (!validate_gemm_args(epilogue, a)) return;
+        launch_gemm_ws(epilogue, a, (hipStream_t)stream);
+    });
+}
+
+int jh_op_pack_ws(const void* w, size_t n, size_t k, void* out) {
+    return jh_guarded([&] {
+        if (!w || !out) throw jh_error(1, "pack_ws: null pointer");
+        if (n == 0 || n % 256 || k == 0 || k % 32 || n * k > ((size_t)1 << 31))
+            throw jh_error(1, "pack_ws: need N % 256 == 0, K % 32 == 0");
+        pack_ws((const bf16_t*)w, (int)n, (int)k, (bf16_t*)out);
+    });
+}
+
 // Gate/up interleave for the GEGLU epilogue (also used by jh_create): 64-row
 // block j holds gate rows [32j, 32j+32) then up rows [inter+32j, inter+32j+32).
 void jh_op_interleave_geglu(const float* wi, size_t inter, size_t k, float* out) {

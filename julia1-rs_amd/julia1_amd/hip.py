@@ -20,7 +20,8 @@ EXPORTS = (
     "jh_collect",
     "jh_set_graph", "jh_set_splitk", "jh_name", "jh_destroy", "jh_last_error", "jh_rope_table", "jh_debug_tokens",
     "jh_debug_encode", "jh_debug_workspace_limit", "jh_profile", "jh_profile_read", "jh_profile_replay",
-    "jh_op_gemm", "jh_op_gemm_splitk", "jh_op_gemm_splitk_noalloc", "jh_op_gemm_ln", "jh_op_interleave_geglu",
+    "jh_op_gemm", "jh_op_gemm_splitk", "jh_op_gemm_splitk_noalloc", "jh_op_gemm_ln", "jh_op_gemm_ws", "jh_op_pack_ws",
+    "jh_op_interleave_geglu",
     "jh_op_embed_ln", "jh_op_layer_norm", "jh_op_final_norm",
     "jh_op_gather_f32", "jh_op_scorer", "jh_op_attention",
 )
@@ -77,6 +78,8 @@ def lib():
                                                 sz, C.c_int, vp]
         L.jh_op_gemm_ln.argtypes = [C.c_int, vp, sz, sz, vp, sz, sz, vp, sz, sz, vp, vp, vp, sz, vp, vp, C.c_float,
                                     vp]
+        L.jh_op_gemm_ws.argtypes = [C.c_int, vp, sz, sz, vp, sz, sz, vp, sz, sz, vp, vp, vp, vp, sz, vp]
+        L.jh_op_pack_ws.argtypes = [vp, sz, sz, vp]
         L.jh_op_interleave_geglu.argtypes = [vp, sz, sz, vp]
         L.jh_op_interleave_geglu.restype = None
         L.jh_op_embed_ln.argtypes = [vp, sz, vp, vp, C.c_float, sz, vp, vp, vp]
@@ -258,6 +261,25 @@ def op_gemm_splitk_noalloc(epi, x, w, out, splits=0, rows=None, gather=None, col
     check(lib().jh_op_gemm_splitk_noalloc(epi, _dp(x), x.stride(0), _dp(gather), rows, _dp(w), n, k, _dp(out),
                                           out.stride(0), col, _dp(bias), _dp(pos), _dp(cos), _dp(sin), rope_cols,
                                           splits, stream))
+
+
+def pack_ws(w):
+    """bf16 torch tensor [n, k] (PyTorch Linear layout; the GEGLU interleave for Wi) -> the same values on the
+    device in the weight-stationary kernel's fragment order (jh_op_pack_ws)."""
+    import torch
+    src = w.detach().to("cpu").contiguous().view(torch.int16).numpy()
+    n, k = src.shape
+    dst = np.empty_like(src)
+    check(lib().jh_op_pack_ws(src.ctypes.data_as(C.c_void_p), n, k, dst.ctypes.data_as(C.c_void_p)))
+    return torch.from_numpy(dst).view(torch.bfloat16).cuda()
+
+
+def op_gemm_ws(epi, x, w_packed, n, k, out, rows=None, col=0, bias=None, pos=None, cos=None, sin=None, rope_cols=0,
+               stream=None):
+    """jh_op_gemm_ws: the weight-stationary GEMM on W packed by pack_ws (K = 768, N % 256 == 0)."""
+    rows = x.shape[0] if rows is None else rows
+    check(lib().jh_op_gemm_ws(epi, _dp(x), x.stride(0), rows, _dp(w_packed), n, k, _dp(out), out.stride(0), col,
+                              _dp(bias), _dp(pos), _dp(cos), _dp(sin), rope_cols, stream))
 
 
 def interleave_geglu(wi: np.ndarray) -> np.ndarray:
