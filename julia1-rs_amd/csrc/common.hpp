@@ -90,22 +90,39 @@ __device__ inline float wave_max(float v) {
 // IEEE division (~10 instructions): the difference, below 2^-22 relative, is
 // far under the approximation's own error and the bf16 rounding of GEGLU.
 __device__ inline float erf_rational(float x) {
+#pragma clang fp contract(off)
     x = fminf(fmaxf(x, -4.0f), 4.0f);
-    float x2 = x * x;
+    const float x2 = x * x;
     float p = -2.72614225801306e-10f;
-    p = p * x2 + 2.77068142495902e-08f;
-    p = p * x2 + -2.10102402082508e-06f;
-    p = p * x2 + -5.69250639462346e-05f;
-    p = p * x2 + -7.34990630326855e-04f;
-    p = p * x2 + -2.95459980854025e-03f;
-    p = p * x2 + -1.60960333262415e-02f;
+    p = __builtin_fmaf(p, x2, 2.77068142495902e-08f);
+    p = __builtin_fmaf(p, x2, -2.10102402082508e-06f);
+    p = __builtin_fmaf(p, x2, -5.69250639462346e-05f);
+    p = __builtin_fmaf(p, x2, -7.34990630326855e-04f);
+    p = __builtin_fmaf(p, x2, -2.95459980854025e-03f);
+    p = __builtin_fmaf(p, x2, -1.60960333262415e-02f);
     float q = -1.45660718464996e-05f;
-    q = q * x2 + -2.13374055278905e-04f;
-    q = q * x2 + -1.68282697438203e-03f;
-    q = q * x2 + -7.37332916720468e-03f;
-    q = q * x2 + -1.42647390514189e-02f;
+    q = __builtin_fmaf(q, x2, -2.13374055278905e-04f);
+    q = __builtin_fmaf(q, x2, -1.68282697438203e-03f);
+    q = __builtin_fmaf(q, x2, -7.37332916720468e-03f);
+    q = __builtin_fmaf(q, x2, -1.42647390514189e-02f);
     return x * p * __builtin_amdgcn_rcpf(q);
 }
 
 // Exact-form GELU 0.5·x·(1 + erf(x/√2)), as nn.GELU() / transformers "gelu".
-__device__ inline float gelu_erf(float x) { return 0.5f * x * (1.0f + erf_rational(x * 0.70710678118654752f)); }
+// Its operations (and erf_rational's) are written out with contraction off, so
+// every inlined copy rounds the same way: an output element is a function of
+// its input alone, whichever kernel or epilogue site computes it.
+__device__ inline float gelu_erf(float x) {
+#pragma clang fp contract(off)
+    return 0.5f * x * (1.0f + erf_rational(x * 0.70710678118654752f));
+}
+
+// Rotate-half RoPE of one (d, d + 32) pair: lo' = lo·c − hi·s, hi' = hi·c + lo·s,
+// each as one rounded product and one fused multiply-add.  Spelling the FMAs
+// out fixes the rounding sequence, so every kernel and every inlined copy (the
+// GEMM epilogues run it at several sites) gives the same bits for a token.
+__device__ inline void rope_rotate(float& lo, float& hi, float c, float s) {
+    const float x0 = lo, x1 = hi;
+    lo = __builtin_fmaf(x0, c, -(x1 * s));
+    hi = __builtin_fmaf(x1, c, x0 * s);
+}

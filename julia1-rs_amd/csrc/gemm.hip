@@ -114,9 +114,10 @@ __device__ inline void epilogue(const GemmArgs& a, f32x16 (&acc)[2][TB], int fw0
                     const f32x4 s = rope_s ? rope_s[j * 4 + qd] : *(const f32x4*)(a.sin_t + p + d);
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
-                        const float x0 = lo[e], x1 = hi[e];
-                        lo[e] = x0 * c[e] - x1 * s[e];
-                        hi[e] = x1 * c[e] + x0 * s[e];
+                        float l = lo[e], h = hi[e];
+                        rope_rotate(l, h, c[e], s[e]);
+                        lo[e] = l;
+                        hi[e] = h;
                     }
                 }
                 putb(tl, d, lo);
@@ -853,9 +854,10 @@ __device__ inline void finish_pair(const GemmArgs& a, long t, int slab, int q, f
             const f32x4 c = *(const f32x4*)(a.cos_t + ps), sn = *(const f32x4*)(a.sin_t + ps);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const float x0 = lo[e], x1 = hi[e];
-                lo[e] = x0 * c[e] - x1 * sn[e];
-                hi[e] = x1 * c[e] + x0 * sn[e];
+                float l = lo[e], h = hi[e];
+                rope_rotate(l, h, c[e], sn[e]);
+                lo[e] = l;
+                hi[e] = h;
             }
         }
         store_bf16(c0, lo);
@@ -1301,9 +1303,11 @@ void launch_cfg(const GemmArgs& a, hipStream_t s) {
         HIP_CHECK(hipGetLastError());
         return;
     }
-    // Weight-stationary kernel when W comes packed for it and each token
-    // range gets at least 64 tokens (its 384 KB W slab per CU is read once).
-    if (gemm_ws_supported(EPI, a) && a.rows >= 64 * gemm_ws_ranges(a)) {
+    // Weight-stationary kernel whenever W comes packed for it, for every
+    // token count: a row's sums then run in one order whatever else is in the
+    // batch (the tiled kernels step K by 16, this one by 32, so switching
+    // kernels on the batch size would move a row's outputs by FP32 rounding).
+    if (gemm_ws_supported(EPI, a)) {
         launch_gemm_ws(EPI, a, s);
         return;
     }

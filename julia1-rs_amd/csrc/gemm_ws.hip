@@ -57,13 +57,6 @@ constexpr int WS_PD = 6;                 // B-fragment reads in flight
 
 __device__ constexpr int swz(int r) { return (r >> 1) & 7; }
 
-// rotate-half RoPE of one (d, d+32) pair, as gemm.hip's epilogue writes it
-__device__ inline void rope_pair(float& lo, float& hi, float c, float s) {
-    const float x0 = lo, x1 = hi;
-    lo = x0 * c - x1 * s;
-    hi = x1 * c + x0 * s;
-}
-
 template <int EPI>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void gemm_ws_kernel(GemmArgs a, int nF,
                                                                                                int R, int nTB) {
@@ -214,7 +207,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
                     e.sn = *(const f32x4*)&S[tk * 32 + ch];
                 } else {
                     float l = e.lo[j - 1], h = e.hi[j - 1];
-                    rope_pair(l, h, e.c[j - 1], e.sn[j - 1]);
+                    rope_rotate(l, h, e.c[j - 1], e.sn[j - 1]);
                     e.lo[j - 1] = l;
                     e.hi[j - 1] = h;
                 }

@@ -162,3 +162,41 @@ def test_pack_ws_layout():
         rw = 64 * (4 * f + wv // 2) + 32 * h + 16 * (wv % 2) + ln % 16
         k0 = 32 * s + 8 * (ln // 16)
         assert np.array_equal(p[f, wv, s, h, ln], src[rw, k0:k0 + 8])
+
+
+@pytest.mark.parametrize("epi", [abi.EPI_ROPE_BF16, abi.EPI_GEGLU_BF16, abi.EPI_RESID_F32, abi.EPI_BIAS_BF16,
+                                 abi.EPI_STORE_BF16])
+def test_ws_rows_independent_of_batch(epi):
+    """A token's outputs are the same bits whatever else is in the batch: rows of sub-batches (config1's first
+    sequence lengths, at their offsets in a 2147-token batch, so a token sits at another place in its 16-token
+    block and its block at another place in its token range) equal the same rows of the full batch.  The
+    encoder's batching invariance (src tests/checkpoint.rs:91-105) rests on this."""
+    g = torch.Generator(device="cuda").manual_seed(40 + epi)
+    subs = [(0, 318), (318, 398), (716, 499), (1215, 263), (1741, 406)]
+    t = 2147
+    x = torch.randn(t, K, device="cuda", generator=g).to(BF16)
+    n = 768 if epi == abi.EPI_RESID_F32 else 2304
+    w = (torch.randn(n, K, device="cuda", generator=g) * 0.02).to(BF16)
+    wp = hip.pack_ws(w)
+    width = n // 2 if epi == abi.EPI_GEGLU_BF16 else n
+    f32 = epi == abi.EPI_RESID_F32
+    base = torch.randn(t, width, device="cuda", generator=g) if f32 else torch.zeros(t, width, dtype=BF16, device="cuda")
+    pos = torch.randint(0, 8192, (t,), device="cuda", generator=g, dtype=torch.int32)
+    cos, sin = (dev(v) for v in oracle.rope_table(10000.0, 8192))
+    bias = torch.randn(n, device="cuda", generator=g) * 0.1
+
+    def run(rows):
+        out = base[rows].clone()
+        kw = {}
+        if epi == abi.EPI_ROPE_BF16:
+            kw = dict(pos=pos[rows].contiguous(), cos=cos, sin=sin, rope_cols=1536)
+        if epi == abi.EPI_BIAS_BF16:
+            kw["bias"] = bias
+        hip.op_gemm_ws(epi, x[rows].contiguous(), wp, n, K, out, **kw)
+        return out
+
+    full = run(slice(0, t))
+    for s0, ln in subs:
+        sub = run(slice(s0, s0 + ln))
+        torch.cuda.synchronize()
+        assert torch.equal(sub, full[s0:s0 + ln]), (s0, ln)
