@@ -17,6 +17,8 @@ from __future__ import annotations
 
 import argparse
 import concurrent.futures as cf
+import json
+import re
 import os
 import shutil
 import subprocess
@@ -50,17 +52,62 @@ def sources():
     return out
 
 
-def compile_one(src: str) -> str:
+RESOURCE_REMARK = "kernel-resource-usage"
+RESOURCES = os.path.join(BUILD, "kernel_resources.json")
+
+
+def kernel_resources(text: str) -> dict:
+    """{kernel: {"vgprs", "agprs", "sgprs", "scratch", "lds"}} from the compiler's
+    -Rpass-analysis=kernel-resource-usage remarks (one "Function Name:" line per
+    kernel followed by its figures)."""
+    keys = {"VGPRs": "vgprs", "AGPRs": "agprs", "SGPRs": "sgprs", "ScratchSize [bytes/lane]": "scratch",
+            "LDS Size [bytes/block]": "lds"}
+    out, cur = {}, None
+    for line in text.splitlines():
+        if RESOURCE_REMARK not in line or "remark:" not in line:
+            continue
+        body = line.split("remark:", 1)[1].rsplit("[-Rpass-analysis", 1)[0].strip()
+        if body.startswith("Function Name:"):
+            cur = body.split(":", 1)[1].strip()
+            out[cur] = {}
+        elif cur is not None and ":" in body:
+            k, v = body.rsplit(":", 1)
+            if k.strip() in keys:
+                out[cur][keys[k.strip()]] = int(v.strip())
+    return out
+
+
+def compile_one(src: str) -> tuple[str, dict]:
     obj = os.path.join(BUILD, os.path.relpath(src, HERE).replace(os.sep, "_") + ".o")
-    lang = ["-x", "hip"] if src.endswith(".hip") else []
+    hip = src.endswith(".hip")
+    lang = ["-x", "hip", f"-Rpass-analysis={RESOURCE_REMARK}"] if hip else []
     cmd = [HIPCC, *FLAGS, *lang, "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
-    msgs = "\n".join(l for l in (r.stdout + r.stderr).splitlines() if "packed-fp32-ops" not in l)
+    text = r.stdout + r.stderr
+    keep, in_remark = [], False
+    for l in text.splitlines():
+        if RESOURCE_REMARK in l:
+            in_remark = True  # the remark and the source excerpt under it
+        elif not (in_remark and re.match(r"^\s*\d*\s*\|", l)):
+            in_remark = False
+            if "packed-fp32-ops" not in l:
+                keep.append(l)
+    msgs = "\n".join(keep)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src}:\n{msgs}")
     if msgs.strip():
         print(msgs, file=sys.stderr)
-    return obj
+    return obj, kernel_resources(text) if hip else {}
+
+
+def check_no_scratch(resources: dict) -> None:
+    """Every kernel keeps its state in registers and LDS: a kernel with per-lane
+    scratch (a private array the compiler could not keep in registers, or
+    spills) fails the build."""
+    bad = {k: v.get("scratch") for k, v in resources.items() if v.get("scratch", 0) != 0}
+    if bad:
+        raise RuntimeError("kernels with per-lane scratch memory: " +
+                           ", ".join(f"{k} ({n} B/lane)" for k, n in sorted(bad.items())))
 
 
 def build(jobs: int | None = None) -> str:
@@ -69,7 +116,14 @@ def build(jobs: int | None = None) -> str:
     srcs = sources()
     jobs = jobs or min(len(srcs), os.cpu_count() or 4, 8)
     with cf.ThreadPoolExecutor(jobs) as ex:
-        objs = list(ex.map(compile_one, srcs))
+        built = list(ex.map(compile_one, srcs))
+    objs = [o for o, _ in built]
+    resources = {}
+    for _, r in built:
+        resources.update(r)
+    with open(RESOURCES, "w") as f:
+        json.dump(resources, f, indent=1, sort_keys=True)
+    check_no_scratch(resources)
     tmp = LIB + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     r = subprocess.run(cmd, capture_output=True, text=True)

@@ -43,8 +43,12 @@ namespace {
 
 constexpr int KT = 64;       // keys per LDS tile
 constexpr int NTHR = 256;   // four waves
-// Lazy rescale threshold (log2 units) and the per-lane sum of 32 p values
-// that proves no p exceeded 2^kLazyLog2 on the fast path: 32 · 2^11 = 2^16.
+// Lazy rescale threshold of the slow path (log2 units: it keeps p <= 2^11),
+// and the bound on a lane's sum of its 32 p values under which the fast path
+// keeps a tile.  The sum bounds each p, so a kept tile has every p <= 2^16:
+// up to 2^5 above the slow path's bound, and still far inside what bf16 P,
+// the FP32 row sums and the FP32 O accumulators carry without overflow or
+// loss of relative precision.
 constexpr float kLazyLog2 = 11.0f;
 constexpr float kSumMax = 65536.0f;
 
@@ -209,9 +213,10 @@ __global__ __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(4))) void 
         const bool edge = a.window >= 0 && (k0 < qlo + 31 - a.window || k0 + KT - 1 > qlo + a.window);
         // Fast path: every key valid and every lane holding a finite running
         // max.  The max of the tile is then not computed at all: a lane's sum
-        // of p bounds each of its p, so a sum within kSumMax proves no p
-        // exceeded 2^kLazyLog2.  Otherwise (a rare tile whose scores rose past
-        // the running max) the tile is redone on the slow path.
+        // of p bounds each of its p, so a sum within kSumMax = 2^16 proves no
+        // p exceeded 2^16.  Otherwise (a rare tile whose scores rose far past
+        // the running max) the tile is redone on the slow path, which moves
+        // the max.
         bool fast = ref_ok && !(tail || edge);
         if (fast) {
             f32x16 s[2];

@@ -652,21 +652,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
         const int lb = ht == BT ? TB : TB - 1;           // 32-token blocks of the loader waves
         const int toff = loader ? 0 : lb * 32;          // this wave's first token in the tile
         const bool full = !loader || ht == BT;          // this wave multiplies all TB blocks
-        // RoPE: this lane's token positions are loaded at the tile's start and
-        // the first 32-token block's cos/sin values during the last K step,
-        // so the epilogue, which every wave of the CU runs at once, does not
-        // start by waiting on two dependent loads (later blocks wait on one).
-        // (256-token tiles keep the loads inside the epilogue: with the
-        // prefetch their registers do not fit two waves per SIMD.)
-        constexpr bool ROPE = EPI == JH_EPI_ROPE_BF16 && TB <= 3;
+        // RoPE with 192-token tiles (RLDS): the loader waves gather the tile's
+        // cos/sin rows into LDS during the last K steps, so the epilogue, which
+        // every wave of the CU runs at once, reads them from LDS instead of
+        // starting on two dependent global loads.  (256-token tiles keep the
+        // loads inside the epilogue: with the staging their registers do not
+        // fit two waves per SIMD.)
+        constexpr bool ROPE = RLDS;
         const bool rot = ROPE && f0 + wf * 64 < a.rope_cols;
-        constexpr bool RGLB = ROPE && !RLDS;  // cos/sin loaded from global memory by each wave
-        int rp[RGLB ? TB : 1];
-        if constexpr (RGLB) {
-#pragma unroll
-            for (int j = 0; j < TB; ++j)
-                rp[j] = rot ? (a.pos[min(t0 + toff + j * 32 + lr, a.rows - 1)] & 0xffff) * 32 : 0;
-        }
         // RLDS: loader wave w gathers table rows [NCS*8*w, NCS*8*(w+1)) of the
         // tile's tokens, lane i row 8j + i/8 of its instruction j, the 16-byte
         // chunk that belongs in slot i%8 of that row under the swizzle.
@@ -713,14 +706,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
                         rs[qd] = *(const f32x4*)&sSin[r * 32 + ((qd * 2 + lg) ^ swz(r)) * 4];
                     }
                 }
-            } else if constexpr (ROPE) {
-                if (rot) {
-#pragma unroll
-                    for (int qd = 0; qd < 4; ++qd) {
-                        rc[qd] = *(const f32x4*)(a.cos_t + rp[j] + qd * 8 + lg * 4);
-                        rs[qd] = *(const f32x4*)(a.sin_t + rp[j] + qd * 8 + lg * 4);
-                    }
-                }
             }
         };
         f32x16 acc[FB][TB];
@@ -734,7 +719,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
             const int st = (base + kt) & 1;
             if (kt > 0 || first) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             __syncthreads();
-            if (!RLDS && kt + 1 == KT) rope_load(0);
             if (loader) {
                 if (kt + 1 < KT) issue(sc, kt + 1, st ^ 1, ht);
                 else if (has_next) issue(sn, 0, st ^ 1, nht);

@@ -72,7 +72,9 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const float* __restrict
 #pragma unroll
     for (int i = 0; i < LN_RPW; ++i) {
         if (row0 + i >= rows) break;
-        r[i].scale_shift(mean[i], RowVec<EPL>::rstd(st[i], eps), g, b ? &bb : nullptr);
+        const float rs = RowVec<EPL>::rstd(st[i], eps);
+        if (b) r[i].scale_shift(mean[i], rs, g, &bb);
+        else r[i].scale_shift(mean[i], rs, g, nullptr);
         r[i].store_bf16(out + (long)(row0 + i) * H, lane);
     }
 }

@@ -62,11 +62,18 @@ struct RowVec {
         }
     }
     // v = (v - mean) * rstd * w (+ b), two-pass statistics over the whole row.
+    // (The bias branch names &bb only where it is loaded: a pointer that may
+    // point at a local or be null keeps that local in scratch memory.)
     __device__ void layer_norm(const float* w, const float* b, float eps, int lane) {
-        RowVec<EPL> g, bb;
+        RowVec<EPL> g;
         g.load(w, lane);
-        if (b) bb.load(b, lane);
-        layer_norm(g, b ? &bb : nullptr, eps);
+        if (b) {
+            RowVec<EPL> bb;
+            bb.load(b, lane);
+            layer_norm(g, &bb, eps);
+        } else {
+            layer_norm(g, nullptr, eps);
+        }
     }
     // The same with the weights (and the bias, when bb is non-null) already
     // loaded, in the steps below.

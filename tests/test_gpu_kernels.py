@@ -151,6 +151,13 @@ def _check_wide_gemm(rows, n, k, epi, seed):
         torch.cuda.synchronize()
         assert (out - (base + prod)).abs().max().item() < 1e-4
         return
+    if epi == abi.EPI_BIAS_F32:
+        bias = torch.randn(n, device="cuda", generator=g) * 0.1
+        out = torch.full((rows, n), float("nan"), device="cuda")
+        hip.op_gemm(epi, x, w, out, bias=bias)
+        torch.cuda.synchronize()
+        assert (out - (prod + bias)).abs().max().item() < 1e-4
+        return
     kw, wk, scale = {}, w, None
     if epi == abi.EPI_GEGLU_BF16:
         inter = n // 2
@@ -205,12 +212,14 @@ def test_gemm_192_token_tiles(rows, n, k, epi):
                                           (23000, 1536, 128, abi.EPI_ROPE_BF16), (15000, 1152, 64, abi.EPI_ROPE_BF16),
                                           (30000, 2304, 64, abi.EPI_GEGLU_BF16),
                                           (12000, 2304, 768, abi.EPI_STORE_BF16), (11000, 1536, 768, abi.EPI_ROPE_BF16),
-                                          (24000, 1152, 256, abi.EPI_GEGLU_BF16)])
+                                          (24000, 1152, 256, abi.EPI_GEGLU_BF16),
+                                          (9482, 2304, 768, abi.EPI_RESID_F32), (12000, 1152, 768, abi.EPI_BIAS_F32)])
 def test_gemm_eight_wave_tiles(rows, n, k, epi):
     """Shapes routed to the eight-wave 256-feature GEMM: 256x192 tiles at config1's 9482 tokens, at the Julia-1
     widths (N = 1152 leaves half a 256-feature tile, whose rows past N read as zeros from the buffer range check)
-    and with token tiles cut at the end, and 256x256 tiles at 32768 tokens; every epilogue family except the FP32
-    residual (N = 768 stays on the four-wave kernels), against torch FP32.  The 23000 / 15000 / 30000 shapes run
+    and with token tiles cut at the end, and 256x256 tiles at 32768 tokens; every epilogue family, the FP32 ones
+    (residual add, bias) at widths that reach this kernel (N = 768 stays on the four-wave kernels), against torch
+    FP32.  The 23000 / 15000 / 30000 shapes run
     one or two K steps per tile with two to four tiles per workgroup, so the next tile's first stage is issued in
     the tile's first step and the RoPE position/cos/sin prefetch runs in the step that also waits on the previous
     epilogue.  Two-phase schedules (a round of full-height tiles, then a round of tiles 32 tokens shorter, whose
@@ -589,6 +598,54 @@ def test_attention_rising_scores(window):
     v = r.standard_normal((t, h))
     qkv = bf16_round(np.concatenate([q, k, v], 1).astype(np.float32))
     q, k, v = qkv[:, :h], qkv[:, h:2 * h], qkv[:, 2 * h:]
+    tiles = _tiles(lens, 128)
+    seqs, start = [], 0
+    for ln in lens:
+        seqs.append((start, ln, start, ln, 0))
+        start += ln
+    expect = _attn_ref64(q, k, v, seqs, heads, window)
+    dq = dev(qkv, BF16)
+    out = torch.zeros(t, h, dtype=BF16, device="cuda")
+    hip.op_attention(dq, 3 * h, dq[:, h:], dq[:, 2 * h:], 3 * h, out, h, dev(np.array(tiles, dtype=np.int32)), heads,
+                     window)
+    got = host(out)
+    assert np.isfinite(got).all()
+    assert np.abs(got - expect).max() < 2e-2, np.abs(got - expect).max()
+
+
+@pytest.mark.parametrize("window", [-1, 512])
+def test_attention_scores_far_above_running_max(window):
+    """Single keys whose scores sit 12 to 15 log2 units above the running max (scores ~0 before them).  The fast
+    path keeps a tile without computing its max while each lane's 32 values of p sum to at most 2^16, so it
+    carries one p of up to 2^15 (keys 70 and 100 share a lane: 2^12 + 2^13.5); two keys at 15.5 units in one
+    lane's 32 (keys 192, 193) exceed the bound and send that tile to the slow path, which moves the max; a spike in a
+    sequence's last, partial tile (key 199 of 200) is masked on the slow path.  Against f64 softmax.  (Window 512
+    covers both sequences, so no tile is a window edge and the fast path runs as for global attention.)"""
+    r = rng(12)
+    heads = 2
+    h = heads * 64
+    lens = [256, 200]
+    t = sum(lens)
+    c = 0.125 * math.log2(math.e)
+    u = np.abs(r.standard_normal(h)) + 0.5
+    q = u[None, :] + 0.05 * r.standard_normal((t, h))
+    k = 0.05 * r.standard_normal((t, h))
+    spikes = [(70, 12.0), (100, 13.5), (150, 15.0), (192, 15.5), (193, 15.5),
+              (256 + 64, 14.0), (256 + 130, 12.5), (256 + 199, 15.0)]
+    for row, d in spikes:
+        for hh in range(heads):
+            uh = u[hh * 64:(hh + 1) * 64]
+            k[row, hh * 64:(hh + 1) * 64] = (d / c) * uh / (uh @ uh)
+    v = r.standard_normal((t, h))
+    qkv = bf16_round(np.concatenate([q, k, v], 1).astype(np.float32))
+    q, k, v = qkv[:, :h], qkv[:, h:2 * h], qkv[:, 2 * h:]
+    # the spikes stand where intended for every query and head (within 0.3 log2 units: the two at 15.5 still sum
+    # past 2^16, a single one at 15 stays below it), the other keys below 1
+    rows = [row for row, _ in spikes]
+    for hh in range(heads):
+        qh, kh = q[:, hh * 64:(hh + 1) * 64].astype(np.float64), k[:, hh * 64:(hh + 1) * 64].astype(np.float64)
+        assert np.abs(c * qh @ kh[rows].T - [d for _, d in spikes]).max() < 0.3
+        assert (c * qh @ np.delete(kh, rows, 0).T).max() < 1.0
     tiles = _tiles(lens, 128)
     seqs, start = [], 0
     for ln in lens:

@@ -1,6 +1,7 @@
 """Host-side checks that need no GPU: the C-ABI library loads and exports
 every function include/*.h declares; the config parser restates
 ModelConfig::from_values; the synthetic generators are deterministic."""
+import json
 import os
 import re
 
@@ -134,3 +135,50 @@ def test_interleave_geglu_layout():
     for j in range(inter // 32):
         assert np.array_equal(out[64 * j:64 * j + 32], wi[32 * j:32 * j + 32])
         assert np.array_equal(out[64 * j + 32:64 * j + 64], wi[inter + 32 * j:inter + 32 * j + 32])
+
+
+def _build_module():
+    import importlib.util
+    path = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "julia1-rs_amd", "build.py")
+    spec = importlib.util.spec_from_file_location("jh_build", path)
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def test_kernel_resource_remarks_parsed_and_scratch_rejected():
+    """The build reads each kernel's figures from hipcc's kernel-resource-usage remarks and fails on any
+    kernel with per-lane scratch."""
+    b = _build_module()
+    text = "\n".join([
+        "x.hip:10:1: remark: Function Name: _Z3fooPf [-Rpass-analysis=kernel-resource-usage]",
+        "   10 | __global__ void foo(float* p) {",
+        "      | ^",
+        "x.hip:10:1: remark:     VGPRs: 24 [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:10:1: remark:     AGPRs: 0 [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:10:1: remark:     ScratchSize [bytes/lane]: 0 [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:10:1: remark:     LDS Size [bytes/block]: 4096 [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:20:1: remark: Function Name: _Z3barPf [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:20:1: remark:     VGPRs: 40 [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:20:1: remark:     ScratchSize [bytes/lane]: 52 [-Rpass-analysis=kernel-resource-usage]",
+    ])
+    r = b.kernel_resources(text)
+    assert r == {"_Z3fooPf": {"vgprs": 24, "agprs": 0, "scratch": 0, "lds": 4096},
+                 "_Z3barPf": {"vgprs": 40, "scratch": 52}}
+    b.check_no_scratch({"_Z3fooPf": r["_Z3fooPf"]})
+    with pytest.raises(RuntimeError, match="_Z3barPf"):
+        b.check_no_scratch(r)
+
+
+def test_built_kernels_use_no_scratch():
+    """The figures the last build recorded: every kernel of the library (the GEMMs, attention, the row
+    kernels) runs without per-lane scratch memory."""
+    b = _build_module()
+    if not os.path.exists(b.RESOURCES):
+        pytest.skip("library not built here")
+    with open(b.RESOURCES) as f:
+        res = json.load(f)
+    names = " ".join(res)
+    for k in ("gemm_ws_kernel", "gemm_big_kernel", "resid_reduce_ln_kernel", "layer_norm_kernel", "attention_kernel"):
+        assert k in names, k
+    assert all(v.get("scratch") == 0 for v in res.values()), {k: v for k, v in res.items() if v.get("scratch")}

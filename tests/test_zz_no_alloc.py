@@ -57,3 +57,58 @@ def test_noalloc_rejects_partials_beyond_scratch():
     with pytest.raises(hip.HipError, match="exceed the 16 MiB scratch") as e:
         hip.op_gemm_splitk_noalloc(abi.EPI_STORE_BF16, x, w, out, splits=8)
     assert e.value.code == abi.JH_ERR_INVALID
+
+
+_CAPTURE_CHILD = r"""
+import sys
+sys.path[:0] = [{root!r}, {pkg!r}]
+import numpy as np
+import torch
+from julia1_amd import abi, hip
+
+BF16 = torch.bfloat16
+r = np.random.default_rng(7)
+rows, n, k = 300, 768, 1152
+x = torch.from_numpy(r.standard_normal((rows, k), dtype=np.float32)).cuda().to(BF16)
+w = (torch.from_numpy(r.standard_normal((n, k), dtype=np.float32)) * 0.02).cuda().to(BF16)
+bias = torch.from_numpy(r.standard_normal(n, dtype=np.float32) * 0.1).cuda()
+out = torch.zeros(rows, n, dtype=BF16, device="cuda")
+x2 = torch.from_numpy(r.standard_normal((70, 768), dtype=np.float32)).cuda().to(BF16)
+w2 = (torch.from_numpy(r.standard_normal((384, 768), dtype=np.float32)) * 0.02).cuda().to(BF16)
+out2 = torch.zeros(70, 384, dtype=BF16, device="cuda")
+torch.cuda.synchronize()
+print("capturing the library's first call", flush=True)
+g = torch.cuda.CUDAGraph()
+with torch.cuda.graph(g):
+    hip.op_gemm_splitk_noalloc(abi.EPI_BIAS_BF16, x, w, out, splits=4, bias=bias,
+                               stream=torch.cuda.current_stream().cuda_stream)
+ws = torch.zeros(64 << 20, dtype=torch.uint8, device="cuda")
+ref = torch.zeros_like(out)
+hip.op_gemm_splitk(abi.EPI_BIAS_BF16, x, w, ref, ws, splits=4, bias=bias)
+torch.cuda.synchronize()
+for i in range(3):
+    out.fill_(float("nan"))
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), i
+    # eager work between replays that rewrites the shared scratch with another call's partials
+    hip.op_gemm_splitk_noalloc(abi.EPI_STORE_BF16, x2, w2, out2, splits=3)
+    torch.cuda.synchronize()
+print("replays match", flush=True)
+"""
+
+
+def test_noalloc_first_call_under_graph_capture():
+    """In a fresh process, the library's first call is jh_op_gemm_splitk_noalloc captured by torch.cuda.graph on
+    torch's capture stream (the scratch address is looked up during the capture); the graph is replayed three
+    times, with an eager no-allocation call on another shape between replays, and every replay equals the
+    workspace entry point's eager output bit for bit."""
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    code = _CAPTURE_CHILD.format(root=root, pkg=os.path.join(root, "julia1-rs_amd"))
+    print("child: noalloc split-K GEMM captured as the first library call", flush=True)
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=110)
+    assert r.returncode == 0 and "replays match" in r.stdout, r.stdout[-2000:] + r.stderr[-2000:]
