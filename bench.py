@@ -10,18 +10,22 @@ lengths U[64,512] from a seed, 2-20 options per row, packed without padding.
 Weights are random-init N(0, 0.02) of the ModernBERT-base shape.
 
 Prints ONE JSON line.  `value` is real (unpadded) tokens per second over the
-K timed steps, with the batch resident in HBM.  `forward_with_pcie_ms` is the
-median of >= 20 whole jh_forward calls (metadata upload, forward, scores
-download) after 3 warm-ups, and `tokens_per_s_with_pcie` its rate.  The
+K timed steps, with the batch resident in HBM (the benchmark contract keeps
+host transfers out of `value`).  `forward_with_pcie_ms` is the median of >= 20
+whole jh_forward calls (metadata upload, forward, scores download) after 3
+warm-ups -- what the reference's own bench times per request -- and
+`tokens_per_s_with_pcie` its rate.  The
 `roofline` object is for the kernel class with the largest device time:
 achieved = its algorithmic FLOPs (2·M·N·K) per launch / its mean in-forward
 launch time over K profiled forwards, each launch timed by events stamped at
 its dispatch on the model's stream (the interval rocprofv3 reports);
 `frac_replay` is the same launch replayed back to back.  `traffic` is the HBM
 bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE runs
-(profiles/traffic.md).  `cpu_baseline` times the FP32 CPU oracle (C++
-restatement of the reference's src/cpu path) on this host's cores, on the
-same batch.  `parity_vs_cpu` compares the GPU's logits with the oracle's
+(profiles/traffic.md, captured on the csrc commit `traffic_csrc_commit`;
+`csrc_commit` is the commit the loaded library was built from).
+`cpu_baseline` times the FP32 CPU oracle (C++ restatement of the reference's
+src/cpu path) on this host's cores, on the same batch, plus configs[3] and
+configs[4] from bounded samples scaled to one forward.  `parity_vs_cpu` compares the GPU's logits with the oracle's
 (julia1_amd.parity: |dlogit|, |dsoftmax|, argmax, top-2 gap histogram).
 """
 from __future__ import annotations
@@ -81,20 +85,36 @@ def roofline(stat, replay_us=None):
     return out
 
 
-def committed_traffic(kernel, workload, roof):
-    """HBM bytes per launch of `kernel` on `workload` from profiles/traffic.md (rocprofv3
-    FETCH_SIZE + WRITE_SIZE per dispatch, calibrated on a plain copy), or None."""
+def committed_traffic(kernel, workload):
+    """(HBM bytes per launch of `kernel` on `workload`, csrc commit it was captured on) from
+    profiles/traffic.md (rocprofv3 FETCH_SIZE + WRITE_SIZE per dispatch, calibrated on a plain copy;
+    its "csrc commit:" line), or (None, commit)."""
     path = os.path.join(ROOT, "profiles", "traffic.md")
     if not os.path.exists(path):
-        return None
+        return None, None
+    traffic, commit = None, None
     for line in open(path):
+        if line.lower().startswith("csrc commit:"):
+            commit = line.split(":", 1)[1].strip().split()[0].strip("`")
         cells = [c.strip() for c in line.strip().strip("|").split("|")]
-        if len(cells) >= 5 and cells[0] == kernel and cells[1] == workload:
+        if traffic is None and len(cells) >= 5 and cells[0] == kernel and cells[1] == workload:
             try:
-                return int(float(cells[4]))
+                traffic = int(float(cells[4]))
             except ValueError:
-                return None
-    return None
+                pass
+    return traffic, commit
+
+
+def build_info():
+    """The csrc commit the loaded library was built from (julia1-rs_amd/lib/build_info.json, written by
+    build.py; "+dirty" when csrc/ differed from it)."""
+    try:
+        with open(os.path.join(ROOT, "julia1-rs_amd", "lib", "build_info.json")) as f:
+            info = json.load(f)
+    except (OSError, ValueError):
+        return None
+    c = info.get("csrc_commit")
+    return None if c is None else c + ("+dirty" if info.get("csrc_dirty") else "")
 
 
 def kernel_table(stats, steps):
@@ -324,7 +344,8 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
-    roof["traffic"] = committed_traffic(roof["kernel"], args.workload, roof)
+    roof["traffic"], roof["traffic_csrc_commit"] = committed_traffic(roof["kernel"], args.workload)
+    roof["csrc_commit"] = build_info()
 
     extra = {}
     if not args.no_extra:
@@ -460,6 +481,22 @@ def main():
                 o.forward(b0)
                 t0.append(time.perf_counter() - tc)
             cpu[key] = round(statistics.median(t0) * 1e3, 2)
+        if not args.no_extra:
+            # configs[3] and configs[4] on the same oracle and threads, each from a bounded sample scaled to one
+            # whole forward: one of config3's four identical 8192-token rows (x4: rows are independent), and
+            # config4's first 64 of 256 rows (x its token ratio: GEMM-dominated at lengths <= 1024; the full
+            # batch measured 19.84 s against 20.07 s so estimated, 16 threads on the MI355X box's host).
+            for wl, sel, how in (("config3", [0], "1 of 4 rows x 4"), ("config4", list(range(64)), "64 of 256 rows")):
+                bw = synth.workload(wl)
+                bs = bw.subset(sel)
+                tc = time.perf_counter()
+                orc.forward(bs)
+                dt = time.perf_counter() - tc
+                est = dt * bw.tokens / bs.tokens
+                cpu[f"{wl}_forward_s"] = round(est, 2)
+                cpu[f"{wl}_tokens_per_s"] = round(bw.tokens / est, 1)
+                cpu[f"{wl}_sample"] = f"{how} ({bs.tokens} of {bw.tokens} tokens) in {dt:.2f} s, scaled by tokens"
+                log(f"cpu oracle: {wl} ~{est:.1f} s/forward ({how}) on {threads} threads")
         cpu["host"] = dict(cpu_model=cpu_model_name(), cpus_visible=len(os.sched_getaffinity(0)),
                            cpus_total=os.cpu_count())
         log(f"cpu oracle: config0 {cpu['config0_ms']} ms/forward on {threads} threads, "

@@ -124,6 +124,7 @@ def build(jobs: int | None = None) -> str:
     with open(RESOURCES, "w") as f:
         json.dump(resources, f, indent=1, sort_keys=True)
     check_no_scratch(resources)
+    write_build_info()
     tmp = LIB + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -132,6 +133,27 @@ def build(jobs: int | None = None) -> str:
     os.replace(tmp, LIB)
     build_static(objs)
     return LIB
+
+
+BUILD_INFO = os.path.join(HERE, "lib", "build_info.json")
+
+
+def write_build_info():
+    """lib/build_info.json: the git commit of the last change under csrc/ and whether csrc/ differs from it, so
+    a run on another machine (which gets the built library without the history) can name what it measured."""
+    info = {"csrc_commit": None, "csrc_dirty": None}
+    try:
+        r = subprocess.run(["git", "-C", ROOT, "log", "-1", "--format=%h", "--", "julia1-rs_amd/csrc"],
+                           capture_output=True, text=True, timeout=20)
+        if r.returncode == 0 and r.stdout.strip():
+            info["csrc_commit"] = r.stdout.strip()
+            d = subprocess.run(["git", "-C", ROOT, "status", "--porcelain", "--", "julia1-rs_amd/csrc"],
+                               capture_output=True, text=True, timeout=20)
+            info["csrc_dirty"] = bool(d.stdout.strip()) if d.returncode == 0 else None
+    except (OSError, subprocess.SubprocessError):
+        pass
+    with open(BUILD_INFO, "w") as f:
+        json.dump(info, f)
 
 
 def _run(cmd, what):
