@@ -208,47 +208,50 @@ __global__ __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(4))) void 
         };
         // Masking is only needed where this wave's (query, key) block can hold
         // an invalid pair (decided per wave, so the branch is uniform): the
-        // sequence end, or a sliding window edge.
+        // sequence end, or a sliding window edge.  Masked scores become -inf,
+        // so their p = exp2(-inf) = 0 on either path.
         const bool tail = k0 + KT > kend;
         const bool edge = a.window >= 0 && (k0 < qlo + 31 - a.window || k0 + KT - 1 > qlo + a.window);
-        // Fast path: every key valid and every lane holding a finite running
-        // max.  The max of the tile is then not computed at all: a lane's sum
-        // of p bounds each of its p, so a sum within kSumMax = 2^16 proves no
-        // p exceeded 2^16.  Otherwise (a rare tile whose scores rose far past
-        // the running max) the tile is redone on the slow path, which moves
-        // the max.
-        bool fast = ref_ok && !(tail || edge);
+        auto mask = [&](f32x16(&s)[2]) {
+            // Element e of block kb is key k0 + kb*32 + (e/4)*8 + 4g + e%4;
+            // element offset off (key kl + off) is valid iff lo <= off <= hi:
+            // off < kend - kl, and |qpos - kl - off| <= window when windowed.
+            const int kl = k0 + 4 * g;  // key of element 0 in block 0 for this lane
+            int lo = 0, hi = kend - kl - 1;
+            if (a.window >= 0) {
+                lo = max(lo, qpos - kl - a.window);
+                hi = min(hi, qpos - kl + a.window);
+            }
+            // Empty range: move lo far right so off - lo wraps to a huge value.
+            const unsigned span = hi >= lo ? (unsigned)(hi - lo) : 0u;
+            lo = hi >= lo ? lo : 0x40000000;
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int off = kb * 32 + (e >> 2) * 8 + (e & 3);
+                    const bool ok = (unsigned)(off - lo) <= span;
+                    s[kb][e] = ok ? s[kb][e] : -INFINITY;
+                }
+        };
+        // Fast path: every lane holding a finite running max (masked tiles
+        // included).  The max of the tile is then not computed at all: a
+        // lane's sum of p bounds each of its p, so a sum within kSumMax = 2^16
+        // proves no p exceeded 2^16.  Otherwise (a rare tile whose scores rose
+        // far past the running max) the tile is redone on the slow path, which
+        // moves the max.
+        bool fast = ref_ok;
         if (fast) {
             f32x16 s[2];
             scores(s);
+            if (tail || edge) mask(s);
             exps(s, m * c);
             fast = __builtin_amdgcn_ballot_w64(!(ls <= kSumMax)) == 0;
         }
         if (!fast) {
             f32x16 s[2];
             scores(s);
-            if (tail || edge) {
-                // Element e of block kb is key k0 + kb*32 + (e/4)*8 + 4g + e%4;
-                // element offset off (key kl + off) is valid iff lo <= off <= hi:
-                // off < kend - kl, and |qpos - kl - off| <= window when windowed.
-                const int kl = k0 + 4 * g;  // key of element 0 in block 0 for this lane
-                int lo = 0, hi = kend - kl - 1;
-                if (a.window >= 0) {
-                    lo = max(lo, qpos - kl - a.window);
-                    hi = min(hi, qpos - kl + a.window);
-                }
-                // Empty range: move lo far right so off - lo wraps to a huge value.
-                const unsigned span = hi >= lo ? (unsigned)(hi - lo) : 0u;
-                lo = hi >= lo ? lo : 0x40000000;
-#pragma unroll
-                for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                    for (int e = 0; e < 16; ++e) {
-                        const int off = kb * 32 + (e >> 2) * 8 + (e & 3);
-                        const bool ok = (unsigned)(off - lo) <= span;
-                        s[kb][e] = ok ? s[kb][e] : -INFINITY;
-                    }
-            }
+            if (tail || edge) mask(s);
             float mx = -INFINITY;
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
