@@ -234,14 +234,24 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
 #pragma unroll
         for (int j = 0; j < 5; ++j) epi_step(e, j, cslot);
     };
+    // The stores go through a buffer resource that ends at the block's last
+    // token, so the range check drops rows past it and no branch is needed:
+    // behind a branch, the compiler sinks the elementwise steps into it, to
+    // the end of the block, away from the MFMA slices they are spread over.
     auto epi_store = [&](EpiState& e) {
-        if (e.t >= a.rows) return;
+        constexpr int ESZ = F32OUT ? 4 : 2;
+        const int t0 = e.t - tk, nt = a.rows - t0 < WS_TB ? a.rows - t0 : WS_TB;
+        const int col = a.col + (GEGLU ? 32 : 64) * hb + x0 + 4 * kg;
+        const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
+            (char*)a.out + (long)t0 * a.ldo * ESZ, 0, nt * a.ldo * ESZ, 0x00020000);
+        const int vo = (tk * a.ldo + col) * ESZ;
         if constexpr (GEGLU) {
-            *(u32x2*)((bf16_t*)a.out + (long)e.t * a.ldo + a.col + 32 * hb + x0 + 4 * kg) =
-                u32x2{pack2(e.lo[0], e.lo[1]), pack2(e.lo[2], e.lo[3])};
+            __builtin_amdgcn_raw_buffer_store_b64(u32x2{pack2(e.lo[0], e.lo[1]), pack2(e.lo[2], e.lo[3])}, ro, vo,
+                                                  0, 0);
         } else if constexpr (F32OUT) {
-            float* o = (float*)a.out + (long)e.t * a.ldo + a.col + 64 * hb + x0 + 4 * kg;
             if constexpr (EPI == JH_EPI_RESID_F32) {
+                // (rows past the last token read the last row: their sums are dropped)
+                const float* o = (const float*)a.out + (long)(e.t < a.rows ? e.t : a.rows - 1) * a.ldo + col;
                 const f32x4 olo = *(const f32x4*)o, ohi = *(const f32x4*)(o + 32);
                 f32x4 lo = e.lo, hi = e.hi;
                 if (a.bias) {
@@ -258,16 +268,17 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
                     lo[i] = olo[i] + lo[i];
                     hi[i] = ohi[i] + hi[i];
                 }
-                *(f32x4*)o = lo;
-                *(f32x4*)(o + 32) = hi;
+                __builtin_amdgcn_raw_buffer_store_b128(lo, ro, vo, 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b128(hi, ro, vo + 32 * ESZ, 0, 0);
             } else {
-                *(f32x4*)o = e.lo;
-                *(f32x4*)(o + 32) = e.hi;
+                __builtin_amdgcn_raw_buffer_store_b128(e.lo, ro, vo, 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b128(e.hi, ro, vo + 32 * ESZ, 0, 0);
             }
         } else {
-            bf16_t* o = (bf16_t*)a.out + (long)e.t * a.ldo + a.col + 64 * hb + x0 + 4 * kg;
-            *(u32x2*)o = u32x2{pack2(e.lo[0], e.lo[1]), pack2(e.lo[2], e.lo[3])};
-            *(u32x2*)(o + 32) = u32x2{pack2(e.hi[0], e.hi[1]), pack2(e.hi[2], e.hi[3])};
+            __builtin_amdgcn_raw_buffer_store_b64(u32x2{pack2(e.lo[0], e.lo[1]), pack2(e.lo[2], e.lo[3])}, ro, vo, 0,
+                                                  0);
+            __builtin_amdgcn_raw_buffer_store_b64(u32x2{pack2(e.hi[0], e.hi[1]), pack2(e.hi[2], e.hi[3])}, ro,
+                                                  vo + 32 * ESZ, 0, 0);
         }
     };
 
@@ -333,8 +344,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
     // Each block starts with a barrier (its X, RoPE rows and positions
     // landed; the slots of two blocks back are free), for which each wave
     // waits for its own DMA, but not for the stores of the epilogue it ran
-    // since: those are its last VMEM instructions, at least 2 of them (1 for
-    // GEGLU; issued since every block has a live token).
+    // since: those are its last VMEM instructions, 2 of them (1 for GEGLU),
+    // issued whether or not their rows are past the last token.
     auto sync = [&](int k) {
         if (k == 1) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         else if constexpr (GEGLU) asm volatile("s_waitcnt vmcnt(1)" ::: "memory");
