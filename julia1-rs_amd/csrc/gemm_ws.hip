@@ -2,7 +2,8 @@
 // and Wo, and the head's K = 768 projections at full batch).
 //
 // out = epi(X · Wᵀ) as in gemm.hip, but each workgroup keeps a 256-row slab
-// of W resident for its whole life (160 VGPRs per lane and 64 KB of LDS) and
+// of W resident for its whole life (160 VGPRs per lane and 64 KB of LDS, or,
+// for the GEGLU epilogue, 192 VGPRs) and
 // streams only X through LDS.  One workgroup per CU, eight waves (two per
 // SIMD); wave w owns 32 W rows as two 16-row blocks ("lo" and "hi") × 768 K,
 // i.e. 48 A-fragments of v_mfma_f32_16x16x32_bf16, and multiplies them with
@@ -46,14 +47,11 @@ namespace {
 
 constexpr int WS_K = 768;
 constexpr int WS_S = WS_K / 32;          // 32-deep K slices
-constexpr int WS_SL = 4;                 // the last WS_SL slices' fragments stay in LDS (registers are the limit)
-constexpr int WS_SR = WS_S - WS_SL;      // slices whose fragments are held in VGPRs
 constexpr int WS_ROWS = 256;             // W rows per workgroup
 constexpr int WS_TB = 16;                // tokens per block
 constexpr int WS_XSLOT = WS_TB * WS_K;   // bf16 elements per X slot (24 KB)
 constexpr int WS_NCS = 3;                // cos/sin and position slots (RoPE)
 constexpr int WS_CSLOT = WS_TB * 32;     // floats per cos (or sin) slot
-constexpr int WS_PD = 6;                 // B-fragment reads in flight
 
 __device__ constexpr int swz(int r) { return (r >> 1) & 7; }
 
@@ -64,8 +62,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
     constexpr bool GEGLU = EPI == JH_EPI_GEGLU_BF16;
     constexpr bool F32OUT = EPI == JH_EPI_RESID_F32 || EPI == JH_EPI_BIAS_F32;
     constexpr bool BIASED = EPI == JH_EPI_BIAS_BF16 || EPI == JH_EPI_BIAS_RELU_BF16 || EPI == JH_EPI_BIAS_F32;
+    // The last WS_SL slices' fragments stay in LDS where the epilogue needs
+    // the registers; GEGLU's fits all 24 slices in VGPRs (and, with fewer
+    // B-fragment reads in flight, its own temporaries).
+    constexpr int WS_SL = GEGLU ? 0 : 4;
+    constexpr int WS_SR = WS_S - WS_SL;   // slices whose fragments are held in VGPRs
+    constexpr int WS_PD = GEGLU ? 3 : 6;  // B-fragment reads in flight
     __shared__ __align__(1024) bf16_t sx[2 * WS_XSLOT];
-    __shared__ __align__(1024) bf16_t swl[8 * WS_SL * 2 * 512];  // each wave's LDS-held fragments
+    __shared__ __align__(1024) bf16_t swl[WS_SL ? 8 * WS_SL * 2 * 512 : 8];  // each wave's LDS-held fragments
     __shared__ __align__(16) float scs[ROPE ? WS_NCS * 2 * WS_CSLOT : 4];
     __shared__ __align__(16) int spos[ROPE ? WS_NCS * 64 : 4];   // token metadata of a block, DMA'd
 
@@ -159,7 +163,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
             wf[s][h] = *(const bf16x8*)(wp + (s * 2 + h) * 512 + lane * 8);
             __builtin_amdgcn_sched_barrier(0);
         }
-    {
+    if constexpr (WS_SL > 0) {
         const i32x4 rw = make_rsrc(wp + WS_SR * 2 * 512, WS_SL * 2 * 1024);
 #pragma unroll
         for (int j = 0; j < WS_SL * 2; ++j) {
@@ -317,7 +321,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
             }
             __builtin_amdgcn_sched_barrier(0);
             if (s + WS_PD < WS_S) bx[s % WS_PD] = rd(s + WS_PD);
-            if (s >= WS_SR - 2 && s < WS_S - 2) {  // LDS-held fragments of slice s + 2 (two buffers)
+            if (WS_SL > 0 && s >= WS_SR - 2 && s < WS_S - 2) {  // LDS-held fragments of slice s + 2 (two buffers)
                 if (decltype(FIRST)::value && s == WS_SR - 2) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
                 const int sl = s + 2 - WS_SR;
 #pragma unroll
