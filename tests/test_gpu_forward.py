@@ -299,6 +299,22 @@ def test_base_long_sequence_8192(base):
     check_gates(s)
 
 
+def test_base_config3_full_batch(base):
+    """The whole configs[3] batch as the bench runs it (4 rows x 8192 tokens, 32768 tokens in one forward)
+    against the oracle on every row, and each row against the same row run alone: the rows share no
+    attention, so a row's scores must not depend on the others beyond the head's batch-size-dependent
+    split-K (within 2e-3, as test_batching_invariance allows)."""
+    ws, gpu, orc = base
+    b = synth.workload("config3")
+    full = gpu.forward(b)
+    s = parity(b, full, orc.forward(b))
+    print("config3", s)
+    check_gates(s)
+    assert s["rows"] == 4
+    alone = np.concatenate([gpu.forward(b.subset([r])) for r in range(4)])
+    assert np.abs(full - alone).max() <= 2e-3
+
+
 def test_profile_replay(tiny):
     """jh_profile_replay times a recorded GEMM/attention launch; staging a batch drops the record."""
     ws, gpu, orc = tiny
