@@ -101,14 +101,17 @@ int jh_op_gemm_ln(int epilogue, const float* xf, size_t ldx, size_t rows, const 
 
 /*
  * jh_op_gemm on the weight-stationary kernel: each workgroup (one per CU)
- * keeps a 256-row slab of W resident (registers and LDS) and streams 16-token
- * blocks of X through LDS, so only X moves from L2 during the multiply.
- * w_packed is W (as jh_op_gemm takes it, [n, k] bf16; the GEGLU interleave
- * for Wi) in the fragment order jh_op_pack_ws writes.  Requires K == 768,
- * N % 256 == 0, no row gather; epilogues and the other arguments as
- * jh_op_gemm.  The same bf16 products as jh_op_gemm, summed in FP32 in K
+ * keeps a slab of W resident (registers and LDS) and streams 16-token blocks
+ * of X through LDS, so only X moves from L2 during the multiply.  w_packed
+ * is W (as jh_op_gemm takes it, [n, k] bf16; the GEGLU interleave for Wi) in
+ * the fragment order jh_op_pack_ws writes.  Shapes: K == 768 with N % 256 ==
+ * 0 (256-row slabs, every epilogue), or K == 1152 with N % 128 == 0 and
+ * JH_EPI_RESID_F32 only (128-row slabs, K split between partner waves whose
+ * two half sums are added lower half first); no row gather.  Other arguments
+ * as jh_op_gemm.  The same bf16 products as jh_op_gemm, summed in FP32 in K
  * order in steps of 32 (jh_op_gemm: 16), so outputs agree to FP32 rounding.
- * jh_forward uses it for the K = 768 GEMMs at full batch.  Replaces cuBLAS
+ * jh_forward uses it for the K = 768 GEMMs and the MLP-out projection
+ * (K = intermediate = 1152) outside the small-batch path.  Replaces cuBLAS
  * gemm_ex (src/cuda/mod.rs:347-375) for those shapes.
  */
 int jh_op_gemm_ws(int epilogue, const void* x, size_t ldx, size_t rows, const void* w_packed, size_t n,
@@ -117,7 +120,8 @@ int jh_op_gemm_ws(int epilogue, const void* x, size_t ldx, size_t rows, const vo
 
 /*
  * Host: reorder a bf16 W [n, k] (row-major) into jh_op_gemm_ws's fragment
- * order (n*k elements; n % 256 == 0, k % 32 == 0).  No reference counterpart
+ * order (n*k elements; k % 32 == 0 and n % 256 == 0, or n % 128 == 0 at
+ * k == 1152, whose layout is the K-split kernel's).  No reference counterpart
  * (a one-time weight layout, as the reference's BF16 conversion at upload,
  * src/cuda/mod.rs:36-39).
  */

@@ -94,10 +94,10 @@ DevBuf upload_bf16(const float* src, size_t n) {
 
 // The same BF16 matrix [n, k] in the weight-stationary GEMM's fragment order
 // (a second copy beside the row-major one, which the other GEMM kernels
-// read), or nothing when that kernel does not take the shape (K != 768 or
-// n % 256 != 0).
+// read), or nothing when that kernel does not take the shape (K = 768 with
+// n % 256 == 0, or K = 1152 with n % 128 == 0).
 DevBuf upload_bf16_ws(const float* src, size_t n, size_t k) {
-    if (k != 768 || n % 256) return DevBuf();
+    if (!((k == 768 && n % 256 == 0) || (k == 1152 && n % 128 == 0))) return DevBuf();
     if (!src) throw jh_error(JH_ERR_INVALID, "missing weight tensor");
     std::vector<bf16_t> tmp(n * k), packed(n * k);
     for (size_t i = 0; i < n * k; ++i) tmp[i] = f2bf_host(src[i]);
@@ -107,7 +107,7 @@ DevBuf upload_bf16_ws(const float* src, size_t n, size_t k) {
 
 struct EncLayer {
     DevBuf attn_norm, wqkv, wo, mlp_norm, wi, wo2;
-    DevBuf wqkv_ws, wo_ws, wi_ws;  // weight-stationary copies (empty where that kernel does not apply)
+    DevBuf wqkv_ws, wo_ws, wi_ws, wo2_ws;  // weight-stationary copies (empty where that kernel does not apply)
     int rope = 0;
     bool global = false;
 };
@@ -548,11 +548,11 @@ struct jh_model {
                  nullptr, nullptr, nullptr, 0, L.wi_ws.as<bf16_t>());
             if (l + 1 < upto && layers[l + 1].attn_norm.p) {
                 gemm_resid_ln(K_WO2, K_LN, hbuf.p, inter, t, L.wo2.as<bf16_t>(), inter, x.as<float>(), nullptr,
-                              layers[l + 1].attn_norm.as<float>(), nullptr, eps, xn.as<bf16_t>());
+                              layers[l + 1].attn_norm.as<float>(), nullptr, eps, xn.as<bf16_t>(), L.wo2_ws.as<bf16_t>());
                 xn_ready = true;
             } else {
                 gemm(K_WO2, JH_EPI_RESID_F32, hbuf.p, inter, nullptr, t, L.wo2.as<bf16_t>(), H, inter, x.p, H, 0,
-                     nullptr);
+                     nullptr, nullptr, nullptr, 0, L.wo2_ws.as<bf16_t>());
             }
         }
     }
@@ -772,6 +772,7 @@ void build_model(jh_model* m, const jh_config* c, const jh_weights* w, int ordin
         L.wi = upload_bf16(wi_tmp.data(), 2 * I * H);
         L.wi_ws = upload_bf16_ws(wi_tmp.data(), 2 * I, H);
         L.wo2 = upload_bf16(s.wo2, H * I);
+        L.wo2_ws = upload_bf16_ws(s.wo2, H, I);
         L.global = c->global[l] != 0;
         const float th = c->rope_theta[l];
         auto it = std::find(thetas.begin(), thetas.end(), th);

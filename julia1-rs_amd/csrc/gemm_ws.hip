@@ -72,6 +72,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
     __shared__ __align__(1024) bf16_t swl[WS_SL ? 8 * WS_SL * 2 * 512 : 8];  // each wave's LDS-held fragments
     __shared__ __align__(16) float scs[ROPE ? WS_NCS * 2 * WS_CSLOT : 4];
     __shared__ __align__(16) int spos[ROPE ? WS_NCS * 64 : 4];   // token metadata of a block, DMA'd
+    constexpr bool RESID = EPI == JH_EPI_RESID_F32;
+    __shared__ __align__(16) f32x4 sold[RESID ? 8 : 1][2][64];   // [wave][lo/hi][lane]: residual rows, by DMA
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -254,9 +256,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
                                                   0, 0);
         } else if constexpr (F32OUT) {
             if constexpr (EPI == JH_EPI_RESID_F32) {
-                // (rows past the last token read the last row: their sums are dropped)
-                const float* o = (const float*)a.out + (long)(e.t < a.rows ? e.t : a.rows - 1) * a.ldo + col;
-                const f32x4 olo = *(const f32x4*)o, ohi = *(const f32x4*)(o + 32);
+                // the residual rows, DMA'd into LDS a block ahead (issue_old)
+                const f32x4 olo = sold[wave][0][lane], ohi = sold[wave][1][lane];
                 f32x4 lo = e.lo, hi = e.hi;
                 if (a.bias) {
                     const f32x4 b_lo = *(const f32x4*)(a.bias + 64 * hb + x0 + 4 * kg);
@@ -283,6 +284,28 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
                                                   0);
             __builtin_amdgcn_raw_buffer_store_b64(u32x2{pack2(e.hi[0], e.hi[1]), pack2(e.hi[2], e.hi[3])}, ro,
                                                   vo + 32 * ESZ, 0, 0);
+        }
+    };
+
+    // RESID: the residual values a wave's lanes add to (block bb, its 16
+    // tokens, columns col .. +3 and col + 32 .. +3) are DMA'd into LDS at the
+    // end of the block, a block ahead of the epilogue that adds them, which
+    // waits for them with an explicit count: a register load would make the
+    // compiler wait with vmcnt(0), and vmcnt completes in order, so that wait
+    // would also wait for the X DMA issued since.  Rows past the last token
+    // read zeros (their sums are dropped by the store's range check).
+    auto issue_old = [&](int bb) {
+        if constexpr (RESID) {
+            const int t0 = bb * WS_TB, nt = a.rows - t0 < WS_TB ? a.rows - t0 : WS_TB;
+            const int col = a.col + 64 * hb + x0 + 4 * kg;
+            const i32x4 ro = make_rsrc((const float*)a.out + (long)t0 * a.ldo, (uint64_t)nt * a.ldo * 4);
+            const uint32_t vo = (uint32_t)(tk * a.ldo + col) * 4;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sold[wave][h][0]);
+                asm volatile("buffer_load_dwordx4 %1, %2, %3 offen lds" ::"{m0}"(m0), "v"(vo), "s"(ro), "s"(h * 128)
+                             : "memory");
+            }
         }
     };
 
@@ -335,10 +358,15 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
             if (s == 9) issue_pos(bb + 2, (k + 2) % WS_NCS);
             if constexpr (decltype(EPI_PREV)::value) {
                 if (s >= 10 && s < 15) epi_step(e, s - 10, (k - 1) % WS_NCS);
-                if (s == 16) epi_store(e);
+                if (s == 16) {
+                    // RESID: the residual rows landed (the 3 X DMA instructions since may not have)
+                    if constexpr (RESID) asm volatile("s_waitcnt vmcnt(3)" ::: "memory");
+                    epi_store(e);
+                }
             }
         }
         __builtin_amdgcn_sched_barrier(0);
+        issue_old(bb);
     };
     using C0 = std::integral_constant<int, 0>;
     using C1 = std::integral_constant<int, 1>;
@@ -349,11 +377,18 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
     // landed; the slots of two blocks back are free), for which each wave
     // waits for its own DMA, but not for the stores of the epilogue it ran
     // since: those are its last VMEM instructions, 2 of them (1 for GEGLU),
-    // issued whether or not their rows are past the last token.
+    // issued whether or not their rows are past the last token; with RESID
+    // the two residual-row DMAs of issue_old follow them (and, in the first
+    // block, come alone).
     auto sync = [&](int k) {
-        if (k == 1) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        else if constexpr (GEGLU) asm volatile("s_waitcnt vmcnt(1)" ::: "memory");
-        else asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+        if constexpr (RESID) {
+            if (k == 1) asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+            else asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+        } else {
+            if (k == 1) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            else if constexpr (GEGLU) asm volatile("s_waitcnt vmcnt(1)" ::: "memory");
+            else asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+        }
         __syncthreads();
     };
     block(C0{}, F{}, T{}, b0);
@@ -379,7 +414,223 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
     if (kl & 1) epi_begin(e, 1, b1 - 1);
     else epi_begin(e, 0, b1 - 1);
     epi_math(e, kl % WS_NCS);
+    if constexpr (RESID) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // its residual rows
     epi_store(e);
+}
+
+// K-split weight-stationary kernel for K = 1152 (the MLP-out projection Wo2,
+// out f32 += X · Wᵀ (+ bias)).  A 256-row slab of K = 1152 (576 KB) does not
+// fit a CU's registers, so each workgroup keeps a 128-row slab and splits K
+// between partner waves: wave w holds rows 32·(w % 4) .. +31 (two 16-row
+// groups, "lo" and "hi") for K slices 18·(w / 4) .. +17, 144 VGPRs.  Per
+// 16-token block each wave runs 36 MFMAs over its half of K (each X fragment
+// feeding both row groups); the upper-half waves (w ≥ 4) leave their sums in
+// LDS at the end of the block, and during the next block the lower-half
+// partner adds them to its own (lower half + upper half, in that order) and
+// runs the residual epilogue.  X streams through two LDS slots as in
+// gemm_ws_kernel (18 stages of [16 rows][128 B] per block, DMA issued by all
+// eight waves between their MFMAs).
+constexpr int W2_K = 1152;
+constexpr int W2_S = W2_K / 32;          // 32-deep K slices
+constexpr int W2_SH = W2_S / 2;          // slices per K half
+constexpr int W2_ROWS = 128;             // W rows per workgroup
+constexpr int W2_XSLOT = WS_TB * W2_K;   // bf16 elements per X slot (36 KB)
+constexpr int W2_XI = W2_K / 64 * 2;     // 1 KB X DMA instructions per block
+constexpr int W2_PD = 6;                 // B-fragment reads in flight
+
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void gemm_ws2_kernel(GemmArgs a, int nF,
+                                                                                                int R, int nTB) {
+    __shared__ __align__(1024) bf16_t sx[2 * W2_XSLOT];
+    __shared__ __align__(16) f32x4 spart[2][4][2][64];  // [block parity][row group][lo/hi][lane]
+    __shared__ __align__(16) f32x4 sold[4][2][64];      // [row group][lo/hi][lane]: residual rows, by DMA
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int rg = wave & 3, kh = wave >> 2;
+    const int G = gridDim.x, bid = blockIdx.x;
+    const int xcd = bid & 7, local = bid >> 3, q8 = G >> 3, r8 = G & 7;
+    const int u = xcd * q8 + (xcd < r8 ? xcd : r8) + local;
+    const int r = u / nF, f = u - r * nF;
+    const int b0 = (int)((long)r * nTB / R), b1 = (int)((long)(r + 1) * nTB / R);
+    if (b0 >= b1) return;
+
+    // X DMA: instruction i (0 .. 35) fills stage i / 2, rows 8(i % 2) .. +7;
+    // wave w issues i = w, w + 8, ... (i % 2 == w % 2), lane j row 8(w % 2) + j / 8.
+    const int drow = 8 * (wave & 1) + (lane >> 3);
+    const uint32_t dchunk = (uint32_t)(((lane & 7) ^ swz(drow)) * 16);
+    const uint32_t xoff = (uint32_t)drow * (uint32_t)a.ldx * 2 + dchunk;
+    auto x_rsrc = [&](int bb) {
+        const int t0 = bb * WS_TB;
+        return bb < b1 ? make_rsrc(a.x + (long)t0 * a.ldx, (uint64_t)(a.rows - 1 - t0) * a.ldx * 2 + (uint64_t)W2_K * 2)
+                       : make_rsrc(a.x, 0);
+    };
+    auto issue_x = [&](const i32x4& rx, int slot, int j) {
+        const int i = wave + 8 * j;
+        if (i < W2_XI) {
+            const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+                (uint32_t)(uintptr_t)&sx[slot * W2_XSLOT + (i >> 1) * 1024 + (i & 1) * 512]);
+            asm volatile("buffer_load_dwordx4 %1, %2, %3 offen lds" ::"{m0}"(m0), "v"(xoff), "s"(rx),
+                         "s"((i >> 1) * 128)
+                         : "memory");
+        }
+    };
+
+    // Prologue: the first block's X ahead of every W load, then this wave's
+    // 36 W fragments in K order (pinned, so the first MFMAs wait for each in turn).
+    {
+        const i32x4 rx = x_rsrc(b0);
+#pragma unroll
+        for (int j = 0; j < 5; ++j) issue_x(rx, 0, j);
+    }
+    __syncthreads();
+    bf16x8 wf[W2_SH][2];
+    const bf16_t* wp = a.w_ws + (long)(f * 8 + wave) * W2_SH * 2 * 512;
+#pragma unroll
+    for (int s = 0; s < W2_SH; ++s)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            wf[s][h] = *(const bf16x8*)(wp + (s * 2 + h) * 512 + lane * 8);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    // the first block's X landed (the 36 W loads issued since may not have)
+    asm volatile("s_waitcnt vmcnt(36)" ::: "memory");
+    __syncthreads();
+
+    const int tk = lane & 15, kg = lane >> 4;
+    const int col = a.col + W2_ROWS * f + 32 * rg + 4 * kg;  // lo columns; hi = col + 16
+    f32x4 acc[2][2];                                          // [set][lo/hi]
+
+    // The residual values a lower-half wave's lanes add to (block bb, its 16
+    // tokens, columns col .. +3 and col + 16 .. +3) are DMA'd into LDS at the
+    // end of the block, a block ahead of the epilogue that adds them; its wait
+    // for them is an explicit count (a register load would make the compiler
+    // wait with vmcnt(0), and vmcnt completes in order: that wait would also
+    // wait for the X DMA issued since).  Rows past the last token read zeros.
+    auto issue_old = [&](int bb) {
+        const int t0 = bb * WS_TB, nt = a.rows - t0 < WS_TB ? a.rows - t0 : WS_TB;
+        const i32x4 ro = make_rsrc((const float*)a.out + (long)t0 * a.ldo, (uint64_t)nt * a.ldo * 4);
+        const uint32_t vo = (uint32_t)(tk * a.ldo + col) * 4;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sold[rg][h][0]);
+            asm volatile("buffer_load_dwordx4 %1, %2, %3 offen lds" ::"{m0}"(m0), "v"(vo), "s"(ro), "s"(h * 64)
+                         : "memory");
+        }
+    };
+    // Residual epilogue of block bb from accumulator set P (lower-half waves,
+    // its residual rows landed in LDS): sum = own + partner's (LDS), + bias,
+    // out = old + sum, through a buffer resource ending at the block's last
+    // token (rows past it are dropped).
+    auto epilogue = [&](int P, int bb) {
+        const int t0 = bb * WS_TB, nt = a.rows - t0 < WS_TB ? a.rows - t0 : WS_TB;
+        const f32x4 plo = spart[(bb - b0) & 1][rg][0][lane], phi = spart[(bb - b0) & 1][rg][1][lane];
+        const f32x4 olo = sold[rg][0][lane], ohi = sold[rg][1][lane];
+        f32x4 lo, hi;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            lo[i] = acc[P][0][i] + plo[i];
+            hi[i] = acc[P][1][i] + phi[i];
+        }
+        if (a.bias) {
+            const f32x4 b_lo = *(const f32x4*)(a.bias + col - a.col), b_hi = *(const f32x4*)(a.bias + col - a.col + 16);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                lo[i] += b_lo[i];
+                hi[i] += b_hi[i];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            lo[i] = olo[i] + lo[i];
+            hi[i] = ohi[i] + hi[i];
+        }
+        const __amdgpu_buffer_rsrc_t ro =
+            __builtin_amdgcn_make_buffer_rsrc((char*)a.out + (long)t0 * a.ldo * 4, 0, nt * a.ldo * 4, 0x00020000);
+        const int vo = (tk * a.ldo + col) * 4;
+        __builtin_amdgcn_raw_buffer_store_b128(lo, ro, vo, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(hi, ro, vo + 64, 0, 0);
+    };
+
+    // One block bb into accumulator set P from X slot (bb - b0) % 2: the
+    // next block's X DMA after slices 1, 3, .., 9 (five instructions for a
+    // lower-half wave); with EPI_PREV the lower-half waves run the previous
+    // block's epilogue after slice 14, once its residual rows (DMA'd before
+    // those five) landed.  At the end the upper-half waves leave this block's
+    // sums in LDS and the lower-half waves issue its residual-row DMA.
+    auto block = [&](auto PC, auto EPI_PREV, int bb) {
+        constexpr int P = decltype(PC)::value;
+        const int k = bb - b0;
+        const bf16_t* X = sx + (k & 1) * W2_XSLOT;
+        auto rd = [&](int s) {
+            const int gs = W2_SH * kh + s, c = (gs & 1) * 4 + kg;
+            return *(const bf16x8*)&X[(gs >> 1) * 1024 + tk * 64 + ((c ^ swz(tk)) * 8)];
+        };
+        const i32x4 rx = x_rsrc(bb + 1);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) acc[P][h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        bf16x8 bx[W2_PD];
+#pragma unroll
+        for (int p = 0; p < W2_PD; ++p) bx[p] = rd(p);
+#pragma unroll
+        for (int s = 0; s < W2_SH; ++s) {
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                acc[P][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[s][h], bx[s % W2_PD], acc[P][h], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            if (s + W2_PD < W2_SH) bx[s % W2_PD] = rd(s + W2_PD);
+            if (s == 1 || s == 3 || s == 5 || s == 7 || s == 9) issue_x(rx, (k + 1) & 1, s >> 1);
+            if constexpr (decltype(EPI_PREV)::value) {
+                if (s == 14 && kh == 0) {
+                    asm volatile("s_waitcnt vmcnt(5)" ::: "memory");
+                    epilogue(1 - P, bb - 1);
+                }
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if (kh == 1) {
+            spart[k & 1][rg][0][lane] = acc[P][0];
+            spart[k & 1][rg][1][lane] = acc[P][1];
+        } else {
+            issue_old(bb);
+        }
+    };
+    using C0 = std::integral_constant<int, 0>;
+    using C1 = std::integral_constant<int, 1>;
+    using T = std::true_type;
+    using F = std::false_type;
+
+    // Each block starts with a barrier: its X landed (each wave waits for its
+    // own DMA, but a lower-half wave not for its last VMEM instructions: the
+    // two stores of its epilogue, none in the first block, and the two
+    // residual-row DMAs after them), the previous block's upper-half sums are
+    // in LDS, and the slots of two blocks back are free.
+    auto sync = [&](int k) {
+        if (kh == 1) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        else if (k == 1) asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+        __syncthreads();
+    };
+    block(C0{}, F{}, b0);
+    int bb = b0 + 1;
+    for (; bb + 1 < b1; bb += 2) {
+        sync(bb - b0);
+        block(C1{}, T{}, bb);
+        sync(bb + 1 - b0);
+        block(C0{}, T{}, bb + 1);
+    }
+    if (bb < b1) {
+        sync(bb - b0);
+        block(C1{}, T{}, bb);
+    }
+    // the last block's upper-half sums and residual rows
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (kh == 0) {
+        if ((b1 - 1 - b0) & 1) epilogue(1, b1 - 1);
+        else epilogue(0, b1 - 1);
+    }
 }
 
 int device_cus() {
@@ -399,22 +650,33 @@ int device_cus() {
 }  // namespace
 
 bool gemm_ws_supported(int epi, const GemmArgs& a) {
-    return a.w_ws && a.k == WS_K && a.n % WS_ROWS == 0 && !a.gather && !a.xf && a.rows > 0 &&
-           ((uintptr_t)a.w_ws & 15) == 0 && epi >= JH_EPI_STORE_BF16 && epi <= JH_EPI_BIAS_F32;
+    if (!a.w_ws || a.gather || a.xf || a.rows <= 0 || ((uintptr_t)a.w_ws & 15)) return false;
+    if (a.k == W2_K) return a.n % W2_ROWS == 0 && epi == JH_EPI_RESID_F32;
+    return a.k == WS_K && a.n % WS_ROWS == 0 && epi >= JH_EPI_STORE_BF16 && epi <= JH_EPI_BIAS_F32;
 }
+
+// W rows per workgroup of the kernel that takes K.
+static int ws_rows(int k) { return k == W2_K ? W2_ROWS : WS_ROWS; }
 
 // Token ranges per slab: as many as fill the CUs (at most one block each).
 int gemm_ws_ranges(const GemmArgs& a) {
-    const int nF = a.n / WS_ROWS, nTB = (a.rows + WS_TB - 1) / WS_TB;
+    const int nF = a.n / ws_rows(a.k), nTB = (a.rows + WS_TB - 1) / WS_TB;
     return std::max(1, std::min(nTB, device_cus() / nF));
 }
 
 int gemm_ws_block_tokens() { return WS_TB; }
 
 void launch_gemm_ws(int epi, const GemmArgs& a, hipStream_t s) {
-    if (!gemm_ws_supported(epi, a)) throw jh_error(1, "gemm: weight-stationary kernel needs packed W, K = 768, N % 256 == 0");
-    const int nF = a.n / WS_ROWS, nTB = (a.rows + WS_TB - 1) / WS_TB, R = gemm_ws_ranges(a);
+    if (!gemm_ws_supported(epi, a))
+        throw jh_error(1, "gemm: weight-stationary kernel needs packed W and K = 768 with N % 256 == 0, or K = 1152 "
+                          "with N % 128 == 0 and the residual epilogue");
+    const int nF = a.n / ws_rows(a.k), nTB = (a.rows + WS_TB - 1) / WS_TB, R = gemm_ws_ranges(a);
     const dim3 grid((unsigned)(nF * R)), block(512);
+    if (a.k == W2_K) {
+        JH_LAUNCH(gemm_ws2_kernel, grid, block, 0, s, a, nF, R, nTB);
+        HIP_CHECK(hipGetLastError());
+        return;
+    }
     switch (epi) {
         case JH_EPI_STORE_BF16: JH_LAUNCH((gemm_ws_kernel<JH_EPI_STORE_BF16>), grid, block, 0, s, a, nF, R, nTB); break;
         case JH_EPI_ROPE_BF16: JH_LAUNCH((gemm_ws_kernel<JH_EPI_ROPE_BF16>), grid, block, 0, s, a, nF, R, nTB); break;
@@ -433,7 +695,22 @@ void launch_gemm_ws(int epi, const GemmArgs& a, hipStream_t s) {
 // Host-side packing of a bf16 [n, k] row-major W into the weight-stationary
 // fragment order: [slab f][wave w][slice s][lo/hi h][lane l][8], lane l
 // holding W row 64(4f + w/2) + 32h + 16(w % 2) + l % 16, K 32s + 8(l/16) .. +8.
+// At K = 1152 (the K-split kernel): 128-row slabs, lane l of wave w holding W
+// row 128f + 32(w % 4) + 16h + l % 16, K 32(18(w / 4) + s) + 8(l/16) .. +8.
 void pack_ws(const bf16_t* w, int n, int k, bf16_t* out) {
+    if (k == W2_K) {
+        for (int f = 0; f < n / W2_ROWS; ++f)
+            for (int wave = 0; wave < 8; ++wave)
+                for (int s = 0; s < W2_SH; ++s)
+                    for (int h = 0; h < 2; ++h)
+                        for (int lane = 0; lane < 64; ++lane) {
+                            const int rw = W2_ROWS * f + 32 * (wave % 4) + 16 * h + lane % 16;
+                            bf16_t* o = out + (((((long)f * 8 + wave) * W2_SH + s) * 2 + h) * 64 + lane) * 8;
+                            const bf16_t* src = w + (long)rw * k + 32 * (W2_SH * (wave / 4) + s) + 8 * (lane / 16);
+                            for (int e = 0; e < 8; ++e) o[e] = src[e];
+                        }
+        return;
+    }
     const int ns = k / 32;
     for (int f = 0; f < n / WS_ROWS; ++f)
         for (int wave = 0; wave < 8; ++wave)

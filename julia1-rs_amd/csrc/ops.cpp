@@ -69,7 +69,8 @@ int jh_op_gemm_ws(int epilogue, const void* x, size_t ldx, size_t rows, const vo
                    as_int(rope_cols, "rope_cols")};
         a.w_ws = (const bf16_t*)w_packed;
         if (!gemm_ws_supported(epilogue, a))
-            throw jh_error(1, "gemm: weight-stationary kernel needs packed W, K = 768, N % 256 == 0");
+            throw jh_error(1, "gemm: weight-stationary kernel needs packed W and K = 768 with N % 256 == 0, or K = "
+                              "1152 with N % 128 == 0 and the residual epilogue");
         if (!validate_gemm_args(epilogue, a)) return;
         launch_gemm_ws(epilogue, a, (hipStream_t)stream);
     });
@@ -78,8 +79,8 @@ int jh_op_gemm_ws(int epilogue, const void* x, size_t ldx, size_t rows, const vo
 int jh_op_pack_ws(const void* w, size_t n, size_t k, void* out) {
     return jh_guarded([&] {
         if (!w || !out) throw jh_error(1, "pack_ws: null pointer");
-        if (n == 0 || n % 256 || k == 0 || k % 32 || n * k > ((size_t)1 << 31))
-            throw jh_error(1, "pack_ws: need N % 256 == 0, K % 32 == 0");
+        if (n == 0 || k == 0 || k % 32 || n * k > ((size_t)1 << 31) || n % (k == 1152 ? 128 : 256))
+            throw jh_error(1, "pack_ws: need K % 32 == 0 and N % 256 == 0 (N % 128 == 0 at K = 1152)");
         pack_ws((const bf16_t*)w, (int)n, (int)k, (bf16_t*)out);
     });
 }

@@ -276,7 +276,8 @@ def pack_ws(w):
 
 def op_gemm_ws(epi, x, w_packed, n, k, out, rows=None, col=0, bias=None, pos=None, cos=None, sin=None, rope_cols=0,
                stream=None):
-    """jh_op_gemm_ws: the weight-stationary GEMM on W packed by pack_ws (K = 768, N % 256 == 0)."""
+    """jh_op_gemm_ws: the weight-stationary GEMM on W packed by pack_ws (K = 768 with N % 256 == 0, or K = 1152
+    with N % 128 == 0 and the residual epilogue)."""
     rows = x.shape[0] if rows is None else rows
     check(lib().jh_op_gemm_ws(epi, _dp(x), x.stride(0), rows, _dp(w_packed), n, k, _dp(out), out.stride(0), col,
                               _dp(bias), _dp(pos), _dp(cos), _dp(sin), rope_cols, stream))

@@ -11,7 +11,10 @@ jh_op_pack_ws) and through jh_op_gemm (the tiled kernels), and requires:
   outputs within 1e-4), so a mistake shared by both kernels is caught too.
 Shapes cover config1's encoder GEMMs (9482 tokens), the M = 16384 sweep, and
 token counts that leave one block per token range, a single workgroup per
-slab, a partial last block, and ranges of unequal length.
+slab, a partial last block, and ranges of unequal length.  At K = 1152 (the
+MLP-out projection, residual epilogue only) the kernel splits K between
+partner waves and adds the upper half's sums to the lower half's through LDS;
+the same checks apply, and rows stay independent of the batch.
 """
 import numpy as np
 import pytest
@@ -28,11 +31,11 @@ BF16 = torch.bfloat16
 K = 768
 
 
-def _case(rows, n, epi, seed, bias=False, col=0, pad_out=0, ldx_pad=0):
+def _case(rows, n, epi, seed, bias=False, col=0, pad_out=0, ldx_pad=0, k=K):
     g = torch.Generator(device="cuda").manual_seed(seed)
-    xs = torch.randn(rows, K + ldx_pad, device="cuda", generator=g).to(BF16)
-    x = xs[:, :K]  # row stride K + ldx_pad
-    w = (torch.randn(n, K, device="cuda", generator=g) * 0.02).to(BF16)
+    xs = torch.randn(rows, k + ldx_pad, device="cuda", generator=g).to(BF16)
+    x = xs[:, :k]  # row stride k + ldx_pad
+    w = (torch.randn(n, k, device="cuda", generator=g) * 0.02).to(BF16)
     prod = x.float() @ w.float().T
     kw = {}
     if epi == abi.EPI_GEGLU_BF16:
@@ -76,7 +79,7 @@ def _case(rows, n, epi, seed, bias=False, col=0, pad_out=0, ldx_pad=0):
         out_ws = torch.zeros(rows, width + col + pad_out, dtype=BF16, device="cuda")
         out_ref = out_ws.clone()
     wp = hip.pack_ws(wk)
-    hip.op_gemm_ws(epi, x, wp, n, K, out_ws, col=col, **kw)
+    hip.op_gemm_ws(epi, x, wp, n, k, out_ws, col=col, **kw)
     hip.op_gemm(epi, x, wk, out_ref, col=col, **kw)
     torch.cuda.synchronize()
     dk = (out_ws.float() - out_ref.float()).abs()
@@ -100,7 +103,7 @@ def _case(rows, n, epi, seed, bias=False, col=0, pad_out=0, ldx_pad=0):
     again = out_ref.clone() if not f32 else base.clone()
     if not f32:
         again.zero_()
-    hip.op_gemm_ws(epi, x, wp, n, K, again, col=col, **kw)
+    hip.op_gemm_ws(epi, x, wp, n, k, again, col=col, **kw)
     torch.cuda.synchronize()
     assert torch.equal(again, out_ws)
 
@@ -200,3 +203,66 @@ def test_ws_rows_independent_of_batch(epi):
         sub = run(slice(s0, s0 + ln))
         torch.cuda.synchronize()
         assert torch.equal(sub, full[s0:s0 + ln]), (s0, ln)
+
+
+K2 = 1152
+
+
+@pytest.mark.parametrize("rows,n", [(1, 768), (17, 768), (1000, 768), (9482, 768), (16384, 768), (30000, 768),
+                                    (2000, 384), (9482, 384)])
+def test_ws_k1152_residual(rows, n):
+    """K = 1152 (Wo2 at hidden 768 and 384): one 16-token block, a partial block, ranges of 1 to 36 blocks, and
+    more token blocks than ranges (30000 tokens: ~45 blocks per range)."""
+    _case(rows, n, abi.EPI_RESID_F32, seed=rows + n, k=K2)
+
+
+def test_ws_k1152_bias_stride_and_column_offset():
+    _case(3001, 768, abi.EPI_RESID_F32, seed=5, bias=True, col=16, pad_out=8, ldx_pad=64, k=K2)
+
+
+def test_ws_k1152_rows_independent_of_batch():
+    """As test_ws_rows_independent_of_batch, for the K-split kernel."""
+    g = torch.Generator(device="cuda").manual_seed(77)
+    subs = [(0, 318), (318, 398), (716, 499), (1215, 263), (1741, 406)]
+    t, n = 2147, 768
+    x = torch.randn(t, K2, device="cuda", generator=g).to(BF16)
+    w = (torch.randn(n, K2, device="cuda", generator=g) * 0.02).to(BF16)
+    wp = hip.pack_ws(w)
+    base = torch.randn(t, n, device="cuda", generator=g)
+
+    def run(rows):
+        out = base[rows].clone()
+        hip.op_gemm_ws(abi.EPI_RESID_F32, x[rows].contiguous(), wp, n, K2, out)
+        return out
+
+    full = run(slice(0, t))
+    for s0, ln in subs:
+        sub = run(slice(s0, s0 + ln))
+        torch.cuda.synchronize()
+        assert torch.equal(sub, full[s0:s0 + ln]), (s0, ln)
+
+
+def test_ws_k1152_rejects_other_epilogues():
+    x = torch.zeros(64, K2, dtype=BF16, device="cuda")
+    wp = hip.pack_ws(torch.zeros(768, K2, dtype=BF16))
+    out = torch.zeros(64, 768, dtype=BF16, device="cuda")
+    with pytest.raises(hip.HipError):
+        hip.op_gemm_ws(abi.EPI_STORE_BF16, x, wp, 768, K2, out)
+    with pytest.raises(hip.HipError):
+        hip.pack_ws(torch.zeros(192, K2, dtype=BF16))
+
+
+def test_pack_ws_layout_k1152():
+    """At K = 1152: slab f (128 rows), wave w, slice s (of its K half), half h, lane l holds W row
+    128f + 32(w % 4) + 16h + l % 16, K 32(18(w / 4) + s) + 8(l/16) .. +8."""
+    n = 384
+    w = torch.arange(n * K2, dtype=torch.int32).remainder(65521).to(torch.int16).view(BF16).reshape(n, K2)
+    p = hip.pack_ws(w).cpu().view(torch.int16).numpy().reshape(n // 128, 8, 18, 2, 64, 8)
+    src = w.view(torch.int16).numpy()
+    rng = np.random.default_rng(6)
+    for _ in range(300):
+        f, wv, s = rng.integers(0, n // 128), rng.integers(0, 8), rng.integers(0, 18)
+        h, ln = rng.integers(0, 2), rng.integers(0, 64)
+        rw = 128 * f + 32 * (wv % 4) + 16 * h + ln % 16
+        k0 = 32 * (18 * (wv // 4) + s) + 8 * (ln // 16)
+        assert np.array_equal(p[f, wv, s, h, ln], src[rw, k0:k0 + 8])
