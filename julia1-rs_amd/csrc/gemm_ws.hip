@@ -74,6 +74,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
     __shared__ __align__(16) int spos[ROPE ? WS_NCS * 64 : 4];   // token metadata of a block, DMA'd
     constexpr bool RESID = EPI == JH_EPI_RESID_F32;
     __shared__ __align__(16) f32x4 sold[RESID ? 8 : 1][2][64];   // [wave][lo/hi][lane]: residual rows, by DMA
+    // [wave][lo/hi][lane]: the bias values of the lane's columns, by DMA in the prologue (a register load in
+    // the epilogue would wait, with vmcnt(0), for the X DMA issued before it)
+    __shared__ __align__(16) f32x4 sbias[BIASED || RESID ? 8 : 1][2][64];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -154,6 +157,19 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
         for (int j = 0; j < 3; ++j) issue_x(rx, 0, j);
         issue_pos(b0, 0);
         if (two) issue_pos(b0 + 1, 1);
+        if constexpr (BIASED || RESID) {
+            if (a.bias) {
+                const int bcol = 64 * (4 * f + (wave >> 1)) + 16 * (wave & 1) + 4 * (lane >> 4);
+                const i32x4 rb = make_rsrc(a.bias, (uint64_t)a.n * 4);
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sbias[wave][h][0]);
+                    asm volatile("buffer_load_dwordx4 %1, %2, %3 offen lds" ::"{m0}"(m0), "v"((uint32_t)bcol * 4),
+                                 "s"(rb), "s"(h * 128)
+                                 : "memory");
+                }
+            }
+        }
     }
     __syncthreads();
     bf16x8 wf[WS_SR][2];
@@ -176,7 +192,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
                          : "memory");
         }
     }
-    // the first block's X and positions landed (48 W loads and DMAs since)
+    // the first block's X, positions and bias landed (48 W loads and DMAs since)
     asm volatile("s_waitcnt vmcnt(48)" ::: "memory");
     __syncthreads();
 
@@ -224,8 +240,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
         }
         if constexpr (BIASED) {
             if (j == 0) {
-                e.c = *(const f32x4*)(a.bias + 64 * hb + x0 + 4 * kg);
-                e.sn = *(const f32x4*)(a.bias + 64 * hb + 32 + x0 + 4 * kg);
+                e.c = sbias[wave][0][lane];
+                e.sn = sbias[wave][1][lane];
             } else {
                 e.lo[j - 1] += e.c[j - 1];
                 e.hi[j - 1] += e.sn[j - 1];
@@ -260,8 +276,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
                 const f32x4 olo = sold[wave][0][lane], ohi = sold[wave][1][lane];
                 f32x4 lo = e.lo, hi = e.hi;
                 if (a.bias) {
-                    const f32x4 b_lo = *(const f32x4*)(a.bias + 64 * hb + x0 + 4 * kg);
-                    const f32x4 b_hi = *(const f32x4*)(a.bias + 64 * hb + 32 + x0 + 4 * kg);
+                    const f32x4 b_lo = sbias[wave][0][lane], b_hi = sbias[wave][1][lane];
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         lo[i] += b_lo[i];
@@ -443,6 +458,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
     __shared__ __align__(1024) bf16_t sx[2 * W2_XSLOT];
     __shared__ __align__(16) f32x4 spart[2][4][2][64];  // [block parity][row group][lo/hi][lane]
     __shared__ __align__(16) f32x4 sold[4][2][64];      // [row group][lo/hi][lane]: residual rows, by DMA
+    __shared__ __align__(16) f32x4 sbias[4][2][64];     // [row group][lo/hi][lane]: bias, by DMA in the prologue
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -481,6 +497,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
         const i32x4 rx = x_rsrc(b0);
 #pragma unroll
         for (int j = 0; j < 5; ++j) issue_x(rx, 0, j);
+        if (a.bias && kh == 0) {
+            const i32x4 rb = make_rsrc(a.bias, (uint64_t)a.n * 4);
+            const uint32_t bo = (uint32_t)(W2_ROWS * f + 32 * rg + 4 * (lane >> 4)) * 4;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sbias[rg][h][0]);
+                asm volatile("buffer_load_dwordx4 %1, %2, %3 offen lds" ::"{m0}"(m0), "v"(bo), "s"(rb), "s"(h * 64)
+                             : "memory");
+            }
+        }
     }
     __syncthreads();
     bf16x8 wf[W2_SH][2];
@@ -492,7 +518,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
             wf[s][h] = *(const bf16x8*)(wp + (s * 2 + h) * 512 + lane * 8);
             __builtin_amdgcn_sched_barrier(0);
         }
-    // the first block's X landed (the 36 W loads issued since may not have)
+    // the first block's X and the bias landed (the 36 W loads issued since may not have)
     asm volatile("s_waitcnt vmcnt(36)" ::: "memory");
     __syncthreads();
 
@@ -532,7 +558,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
             hi[i] = acc[P][1][i] + phi[i];
         }
         if (a.bias) {
-            const f32x4 b_lo = *(const f32x4*)(a.bias + col - a.col), b_hi = *(const f32x4*)(a.bias + col - a.col + 16);
+            const f32x4 b_lo = sbias[rg][0][lane], b_hi = sbias[rg][1][lane];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 lo[i] += b_lo[i];
