@@ -446,15 +446,18 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
 // gemm_ws_kernel (18 stages of [16 rows][128 B] per block, DMA issued by all
 // eight waves between their MFMAs).
 constexpr int W2_K = 1152;
-constexpr int W2_S = W2_K / 32;          // 32-deep K slices
-constexpr int W2_SH = W2_S / 2;          // slices per K half
 constexpr int W2_ROWS = 128;             // W rows per workgroup
-constexpr int W2_XSLOT = WS_TB * W2_K;   // bf16 elements per X slot (36 KB)
-constexpr int W2_XI = W2_K / 64 * 2;     // 1 KB X DMA instructions per block
 constexpr int W2_PD = 6;                 // B-fragment reads in flight
 
+template <int KS>  // 32-deep K slices
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void gemm_ws2_kernel(GemmArgs a, int nF,
                                                                                                 int R, int nTB) {
+    constexpr int W2_K = KS * 32;
+    constexpr int W2_SH = KS / 2;            // slices per K half
+    constexpr int W2_XSLOT = WS_TB * W2_K;   // bf16 elements per X slot
+    constexpr int W2_XI = W2_K / 64 * 2;     // 1 KB X DMA instructions per block
+    constexpr int W2_NXL = (W2_XI - 4) / 8 + 1;  // of which a lower-half wave (w < 4) issues
+    constexpr int W2_ES = W2_SH - 4;         // slice after which the previous block's epilogue runs
     __shared__ __align__(1024) bf16_t sx[2 * W2_XSLOT];
     __shared__ __align__(16) f32x4 spart[2][4][2][64];  // [block parity][row group][lo/hi][lane]
     __shared__ __align__(16) f32x4 sold[4][2][64];      // [row group][lo/hi][lane]: residual rows, by DMA
@@ -519,7 +522,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
             __builtin_amdgcn_sched_barrier(0);
         }
     // the first block's X and the bias landed (the 36 W loads issued since may not have)
-    asm volatile("s_waitcnt vmcnt(36)" ::: "memory");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * W2_SH) : "memory");
     __syncthreads();
 
     const int tk = lane & 15, kg = lane >> 4;
@@ -608,8 +611,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
             if (s + W2_PD < W2_SH) bx[s % W2_PD] = rd(s + W2_PD);
             if (s == 1 || s == 3 || s == 5 || s == 7 || s == 9) issue_x(rx, (k + 1) & 1, s >> 1);
             if constexpr (decltype(EPI_PREV)::value) {
-                if (s == 14 && kh == 0) {
-                    asm volatile("s_waitcnt vmcnt(5)" ::: "memory");
+                if (s == W2_ES && kh == 0) {
+                    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(W2_NXL) : "memory");
                     epilogue(1 - P, bb - 1);
                 }
             }
@@ -699,7 +702,7 @@ void launch_gemm_ws(int epi, const GemmArgs& a, hipStream_t s) {
     const int nF = a.n / ws_rows(a.k), nTB = (a.rows + WS_TB - 1) / WS_TB, R = gemm_ws_ranges(a);
     const dim3 grid((unsigned)(nF * R)), block(512);
     if (a.k == W2_K) {
-        JH_LAUNCH(gemm_ws2_kernel, grid, block, 0, s, a, nF, R, nTB);
+        JH_LAUNCH((gemm_ws2_kernel<W2_K / 32>), grid, block, 0, s, a, nF, R, nTB);
         HIP_CHECK(hipGetLastError());
         return;
     }
@@ -725,6 +728,7 @@ void launch_gemm_ws(int epi, const GemmArgs& a, hipStream_t s) {
 // row 128f + 32(w % 4) + 16h + l % 16, K 32(18(w / 4) + s) + 8(l/16) .. +8.
 void pack_ws(const bf16_t* w, int n, int k, bf16_t* out) {
     if (k == W2_K) {
+        const int W2_SH = k / 64;
         for (int f = 0; f < n / W2_ROWS; ++f)
             for (int wave = 0; wave < 8; ++wave)
                 for (int s = 0; s < W2_SH; ++s)
