@@ -395,8 +395,9 @@ def main():
                 out = torch.zeros(M, n // 2, dtype=torch.bfloat16, device="cuda")
             else:
                 out = torch.zeros(M, n, dtype=torch.bfloat16, device="cuda")
-            # K = 768 runs the weight-stationary kernel on a packed W, as the forward does; K = 1152 the tiled one.
-            use_ws = k == 768
+            # Every shape runs the weight-stationary kernel on a packed W, as the forward does (K = 1152: the
+            # K-split form, residual epilogue).
+            use_ws = k == 768 or (k == 1152 and epi == abi.EPI_RESID_F32)
             Wp = hip.pack_ws(W) if use_ws else None
 
             def run_once():
@@ -418,7 +419,9 @@ def main():
             byts = M * k * 2 + n * k * 2 + (M * n * 8 if epi == abi.EPI_RESID_F32 else
                                            M * n // 2 * 2 if epi == abi.EPI_GEGLU_BF16 else M * n * 2)
             tf = fl / (ms * 1e-3) / 1e12
-            sweep.append(dict(gemm=name, M=M, N=n, K=k, kernel="weight-stationary" if use_ws else "tiled",
+            sweep.append(dict(gemm=name, M=M, N=n, K=k,
+                              kernel=("weight-stationary, K split" if k == 1152 else "weight-stationary") if use_ws
+                              else "tiled",
                               us=round(ms * 1e3, 2), tflops=round(tf, 1),
                               mfma_frac=round(tf / PEAK_BF16_TFLOPS, 4),
                               roofline_frac=round(max(fl / (PEAK_BF16_TFLOPS * 1e12), byts / (PEAK_HBM_GBS * 1e9))
