@@ -20,9 +20,12 @@ achieved = its algorithmic FLOPs (2·M·N·K) per launch / its mean in-forward
 launch time over K profiled forwards, each launch timed by events stamped at
 its dispatch on the model's stream (the interval rocprofv3 reports);
 `frac_replay` is the same launch replayed back to back.  `traffic` is the HBM
-bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE runs
-(profiles/traffic.md, captured on the csrc commit `traffic_csrc_commit`;
-`csrc_commit` is the commit the loaded library was built from).
+bytes per launch, counted in this run by two short child runs of this bench
+under rocprofv3 --pmc (FETCH_SIZE, then WRITE_SIZE, each calibrated on a plain
+256 MiB copy), before the parent touches the GPU; the committed figure of
+profiles/traffic.md is kept beside it (`traffic_committed`) and used when the
+live count is not possible (`traffic_source` says which).  `csrc_commit` is
+the commit the loaded library was built from.
 `cpu_baseline` times the FP32 CPU oracle (C++ restatement of the reference's
 src/cpu path) on this host's cores, on the same batch, plus configs[3] and
 configs[4] from bounded samples scaled to one forward.  `parity_vs_cpu` compares the GPU's logits with the oracle's
@@ -103,6 +106,62 @@ def committed_traffic(kernel, workload):
             except ValueError:
                 pass
     return traffic, commit
+
+
+# Kernel classes whose launches have a kernel symbol of their own in a config1 forward, so their counters can
+# be told apart in a rocprofv3 run (the Wo class shares gemm_ws_kernel<3> with the head's out_proj, and the
+# attention classes share attention_kernel).
+TRAFFIC_SYMBOL = {"gemm_qkv_rope": "gemm_ws_kernel<1>", "gemm_wi_geglu": "gemm_ws_kernel<2>",
+                  "gemm_wo2_resid": "gemm_ws2_kernel<36>"}
+
+
+def live_traffic(workload):
+    """HBM bytes per launch of the TRAFFIC_SYMBOL classes on `workload`, measured in this run: two child runs
+    of this bench under `rocprofv3 --pmc` (FETCH_SIZE, then WRITE_SIZE, one counter per run), each value scaled
+    by what the same counter reads for a plain 256 MiB device-to-device copy in the same child (--copy-probe).
+    Means over the children's in-forward launches; the 51 replays of their dominant launch, which come last
+    before the copies, are left out.  To be called before this process touches the GPU.  Returns
+    ({class: bytes}, note); the dict is empty when rocprofv3 is absent or a run gives no counter file."""
+    import csv
+    import shutil
+    import subprocess
+    import tempfile
+    exe = shutil.which("rocprofv3")
+    if exe is None:
+        return {}, "rocprofv3 not found"
+    tmp = tempfile.mkdtemp(prefix="jh_traffic_")
+    per = {}
+    for ctr in ("FETCH_SIZE", "WRITE_SIZE"):
+        d = os.path.join(tmp, ctr)
+        cmd = [exe, "--pmc", ctr, "--output-format", "csv", "-d", d, "-o", "m", "--", sys.executable, "-u",
+               os.path.abspath(__file__), "--no-cpu", "--no-extra", "--steps", "3", "--warmup", "1",
+               "--copy-probe", "256", "--workload", workload]
+        log(f"traffic: rocprofv3 --pmc {ctr} over a short run of this bench")
+        with open(os.path.join(tmp, ctr + ".log"), "w") as lf:
+            # own process group, so that a time-out also ends the profiled python under rocprofv3
+            p = subprocess.Popen(cmd, stdout=lf, stderr=subprocess.STDOUT, cwd=ROOT, start_new_session=True)
+            try:
+                rc = p.wait(timeout=150)
+            except subprocess.TimeoutExpired:
+                os.killpg(p.pid, 9)
+                p.wait()
+                return {}, f"{ctr} run timed out"
+        path = os.path.join(d, "m_counter_collection.csv")
+        if not os.path.exists(path):  # (rocprofv3 may exit 139 after complete results; the file decides)
+            return {}, f"{ctr} run gave no counter file (rc {rc})"
+        with open(path) as f:
+            rows = sorted(csv.DictReader(f), key=lambda r: int(r["Dispatch_Id"]))
+        copies = sorted(float(r["Counter_Value"]) for r in rows if "copyBuffer" in r["Kernel_Name"])[-3:]
+        kern = [r for r in rows if "copyBuffer" not in r["Kernel_Name"]][:-51]
+        if len(copies) < 3 or min(copies) <= 0:
+            return {}, f"{ctr} run has no copy calibration"
+        scale = 256 * 1024 / statistics.mean(copies) * 1024  # counter units -> bytes
+        for cls, sym in TRAFFIC_SYMBOL.items():
+            vals = [float(r["Counter_Value"]) for r in kern if sym in r["Kernel_Name"]]
+            if vals:
+                per.setdefault(cls, {})[ctr] = statistics.mean(vals) * scale
+    total = {c: int(round(v["FETCH_SIZE"] + v["WRITE_SIZE"])) for c, v in per.items() if len(v) == 2}
+    return total, "rocprofv3 --pmc FETCH_SIZE + WRITE_SIZE in two child runs of this bench, copy-calibrated"
 
 
 def build_info():
@@ -274,6 +333,12 @@ def main():
                           "n_gpus": args.gpus, "skipped": True}))
         sys.exit(2)
 
+    # HBM traffic of the dominant kernel, counted live before this process touches the GPU (not when this
+    # run is itself under a profiler, or a short run without the extra workloads).
+    traffic_live, traffic_note = {}, "not measured in this run"
+    if not (args.no_extra or args.protocol_only or any(k.startswith("ROCPROF") for k in os.environ)):
+        traffic_live, traffic_note = live_traffic(args.workload)
+
     import numpy as np
     import torch
     from julia1_amd import abi, hip, synth
@@ -344,8 +409,15 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
-    roof["traffic"], roof["traffic_csrc_commit"] = committed_traffic(roof["kernel"], args.workload)
     roof["csrc_commit"] = build_info()
+    committed, committed_commit = committed_traffic(roof["kernel"], args.workload)
+    if roof["kernel"] in traffic_live:
+        roof["traffic"], roof["traffic_source"] = traffic_live[roof["kernel"]], traffic_note
+        roof["traffic_csrc_commit"] = roof["csrc_commit"]
+        roof["traffic_committed"], roof["traffic_committed_csrc_commit"] = committed, committed_commit
+    else:
+        roof["traffic"], roof["traffic_csrc_commit"] = committed, committed_commit
+        roof["traffic_source"] = f"profiles/traffic.md ({traffic_note})"
 
     extra = {}
     if not args.no_extra:
