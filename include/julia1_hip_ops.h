@@ -196,6 +196,18 @@ int jh_op_attention(const void* q, size_t ldq, const void* k, const void* v, siz
                     void* out, size_t ldo, const jh_attn_tile* tiles, size_t ntiles,
                     size_t heads, int window, float scale, void* stream);
 
+/*
+ * jh_op_attention with work items of up to 256 queries (tiles of nq <= 256):
+ * eight waves per (tile, head), each staged K/V tile shared by twice the
+ * queries.  The backend uses it for the global layers of sequences of 4096
+ * tokens or more.  Same arithmetic per query as jh_op_attention.  No separate
+ * counterpart in the reference (part of attention_rope/attention_plain,
+ * src/cuda/kernels.cu:274-391).
+ */
+int jh_op_attention_wide(const void* q, size_t ldq, const void* k, const void* v, size_t ldkv,
+                         void* out, size_t ldo, const jh_attn_tile* tiles, size_t ntiles,
+                         size_t heads, int window, float scale, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

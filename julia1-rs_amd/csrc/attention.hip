@@ -42,7 +42,6 @@
 namespace {
 
 constexpr int KT = 64;       // keys per LDS tile
-constexpr int NTHR = 256;   // four waves
 // Lazy rescale threshold of the slow path (log2 units: it keeps p <= 2^11),
 // and the bound on a lane's sum of its 32 p values under which the fast path
 // keeps a tile.  The sum bounds each p, so a kept tile has every p <= 2^16:
@@ -63,7 +62,13 @@ typedef __attribute__((address_space(3))) uint8_t lds_u8;
 __device__ constexpr int kswz(int r) { return (r >> 1) & 7; }
 __device__ constexpr int vswz(int r) { return ((r >> 1) & 1) << 2; }
 
-__global__ __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(4))) void attention_kernel(AttnArgs a) {
+// NW waves per workgroup, 32 queries each: 4 (128-query tiles) everywhere, or
+// 8 (256-query tiles) for the global layers of long sequences, where each
+// staged K/V tile then serves twice the queries (global layer at 4 x 8192:
+// 2% faster; slower for sequences of ~1k tokens and for window layers).
+template <int NW>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) void attention_kernel(AttnArgs a) {
+    constexpr int RPW = KT / NW;  // K/V rows each wave stages per tile (8 per DMA instruction)
     __shared__ __align__(1024) bf16_t sK[2][KT * 64];
     __shared__ __align__(1024) bf16_t sV[2][KT * 64];
 
@@ -102,27 +107,27 @@ __global__ __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(4))) void 
         kend = min(tile.kv_len, tile.q_pos + tile.nq + a.window);
     }
 
-    // DMA of one K/V tile into buffer `buf`: wave w fills rows [16w, 16w+16)
-    // of both with two 1 KB instructions each; lane i of instruction j takes
-    // row 16w + 8j + i/8, physical slot i%8.  The lane's byte offsets are
+    // DMA of one K/V tile into buffer `buf`: wave w fills rows [RPW·w, RPW·w+RPW)
+    // of both with RPW/8 1 KB instructions each; lane i of instruction j takes
+    // row RPW·w + 8j + i/8, physical slot i%8.  The lane's byte offsets are
     // fixed per row (the tile adds k0 rows); rows past the sequence end fall
     // outside the buffer resource's range and read as zeros (they are masked
     // to -inf before the softmax, and their zero V rows contribute nothing).
     const i32x4 rsk = make_rsrc(kbase, ((uint64_t)(tile.kv_len - 1) * a.ldkv + 64) * 2);
     const i32x4 rsv = make_rsrc(vbase, ((uint64_t)(tile.kv_len - 1) * a.ldkv + 64) * 2);
     const uint32_t lk0 = (uint32_t)(uintptr_t)&sK[0][0], lv0 = (uint32_t)(uintptr_t)&sV[0][0];
-    uint32_t okb[2], ovb[2];
+    uint32_t okb[RPW / 8], ovb[RPW / 8];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int row = 16 * wave + 8 * j + (lane >> 3);
+    for (int j = 0; j < RPW / 8; ++j) {
+        const int row = RPW * wave + 8 * j + (lane >> 3);
         okb[j] = (uint32_t)(row * a.ldkv + (((lane & 7) ^ kswz(row)) * 8)) * 2;
         ovb[j] = (uint32_t)(row * a.ldkv + (((lane & 7) ^ vswz(row)) * 8)) * 2;
     }
     auto issue = [&](int k0, int buf) {
         const uint32_t kt = (uint32_t)(k0 * a.ldkv) * 2;  // bytes of the tile's first key row
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int r0 = 16 * wave + 8 * j;
+        for (int j = 0; j < RPW / 8; ++j) {
+            const int r0 = RPW * wave + 8 * j;
             const uint32_t lk = __builtin_amdgcn_readfirstlane(lk0 + (buf * KT * 64 + r0 * 64) * 2);
             const uint32_t lv = __builtin_amdgcn_readfirstlane(lv0 + (buf * KT * 64 + r0 * 64) * 2);
             asm volatile("buffer_load_dwordx4 %1, %2, 0 offen lds" ::"{m0}"(lk), "v"(okb[j] + kt), "s"(rsk)
@@ -319,12 +324,14 @@ __global__ __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(4))) void 
 
 void launch_attention(const AttnArgs& a, hipStream_t s) {
     if (a.ntiles < 0 || a.heads <= 0) throw jh_error(1, "attention: bad tile/head count");
+    if (a.waves != 4 && a.waves != 8) throw jh_error(1, "attention: 4 or 8 waves (128- or 256-query tiles)");
     if (a.ntiles == 0) return;
     if (!a.q || !a.k || !a.v || !a.out || !a.tiles) throw jh_error(1, "attention: null operand");
     if (a.ldq % 8 || a.ldkv % 8 || a.ldo % 4 || a.ldq < a.heads * 64 || a.ldo < a.heads * 64 ||
         ((uintptr_t)a.q & 15) || ((uintptr_t)a.k & 15) || ((uintptr_t)a.v & 15) || ((uintptr_t)a.out & 7))
         throw jh_error(1, "attention: operands must be 16-byte aligned with row strides % 8 == 0");
     if ((long)a.ntiles * a.heads > 0x7fffffffL) throw jh_error(1, "attention: grid too large");
-    JH_LAUNCH(attention_kernel, dim3((unsigned)(a.ntiles * a.heads)), dim3(NTHR), 0, s, a);
+    if (a.waves == 8) JH_LAUNCH(attention_kernel<8>, dim3((unsigned)(a.ntiles * a.heads)), dim3(512), 0, s, a);
+    else JH_LAUNCH(attention_kernel<4>, dim3((unsigned)(a.ntiles * a.heads)), dim3(256), 0, s, a);
     HIP_CHECK(hipGetLastError());
 }

@@ -165,9 +165,9 @@ struct MetaSlot {
     size_t markers = 0;
     // graph of the launch sequence for the shape staged in this slot
     hipGraphExec_t graph = nullptr;
-    size_t graph_key[6] = {0, 0, 0, 0, 0, 0};
+    size_t graph_key[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     // shape of the previous execute from this slot: captured only when it repeats
-    size_t last_key[6] = {0, 0, 0, 0, 0, 0};
+    size_t last_key[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 };
 
 }  // namespace
@@ -206,6 +206,14 @@ struct jh_model {
     uint32_t* d_tok = nullptr;
     AttnTile* d_tiles = nullptr;
     AttnTile* d_mtiles = nullptr;
+    // Global layers of sequences of kLongSeq tokens or more run 256-query
+    // work items of eight waves (d_gtiles[0, nglong)); the other sequences'
+    // 128-query tiles follow (d_gtiles[nglong, nglong + ngshort)).  With no
+    // long sequence, global layers use d_tiles.
+    static constexpr uint32_t kLongSeq = 4096;
+    AttnTile* d_gtiles = nullptr;
+    size_t nglong = 0, ngshort = 0;
+    double pairs_glong = 0, pairs_gshort = 0, rows_glong = 0;
     int32_t* d_markers = nullptr;
     // replay repeated shapes from a captured graph (see jh_set_graph)
     bool use_graph = true;
@@ -352,6 +360,26 @@ struct jh_model {
         std::stable_sort(tiles.begin(), tiles.end(), [](const AttnTile& x, const AttnTile& y) {
             return (int64_t)x.nq * x.kv_len > (int64_t)y.nq * y.kv_len;
         });
+        // Global-layer lists when some sequence is long: its 256-query tiles
+        // first (costliest first), then the 128-query tiles of the others, in
+        // the order of `tiles`.
+        std::vector<AttnTile> gtiles;
+        size_t glong = 0;
+        bool any_long = false;
+        for (size_t s = 0; s < nseq; ++s) any_long |= lens[s] >= kLongSeq;
+        if (any_long) {
+            for (size_t s = 0; s < nseq; ++s)
+                if (lens[s] >= kLongSeq)
+                    for (uint32_t q0 = 0; q0 < lens[s]; q0 += 2 * QTILE)
+                        gtiles.push_back({(int32_t)(starts[s] + q0), (int32_t)std::min<uint32_t>(2 * QTILE, lens[s] - q0),
+                                          (int32_t)starts[s], (int32_t)lens[s], (int32_t)q0});
+            std::stable_sort(gtiles.begin(), gtiles.end(), [](const AttnTile& x, const AttnTile& y) {
+                return (int64_t)x.nq * x.kv_len > (int64_t)y.nq * y.kv_len;
+            });
+            glong = gtiles.size();
+            for (const AttnTile& tl : tiles)
+                if ((uint32_t)tl.kv_len < kLongSeq) gtiles.push_back(tl);
+        }
         size_t mi = 0;
         for (size_t s = 0; s < nseq; ++s) {
             size_t first = mi;
@@ -361,7 +389,7 @@ struct jh_model {
                                   (int32_t)lens[s], 0});
         }
         if (mi != m) throw jh_error(JH_ERR_INVALID, "marker rows must lie in their sequence, grouped by sequence");
-        const size_t meta_len = 2 * t + 5 * (tiles.size() + mtiles.size()) + m;
+        const size_t meta_len = 2 * t + 5 * (tiles.size() + mtiles.size()) + m + 5 * gtiles.size();
         ensure_workspace(t, m, slot, meta_len);
         MetaSlot& ms = slots[slot];
         // The slot's previous upload may still be reading its pinned staging buffer.
@@ -376,6 +404,7 @@ struct jh_model {
         std::memcpy(hm_ + 2 * t, tiles.data(), tiles.size() * sizeof(AttnTile));
         std::memcpy(hm_ + 2 * t + 5 * tiles.size(), mtiles.data(), mtiles.size() * sizeof(AttnTile));
         std::memcpy(hm_ + 2 * t + 5 * (tiles.size() + mtiles.size()), marker_rows, m * 4);
+        std::memcpy(hm_ + 2 * t + 5 * (tiles.size() + mtiles.size()) + m, gtiles.data(), gtiles.size() * sizeof(AttnTile));
         HIP_CHECK(hipMemcpyAsync(ms.dev.p, ms.host.p, meta_len * 4, hipMemcpyHostToDevice, stream));
         HIP_CHECK(hipEventRecord(ms.uploaded, stream));
         ms.upload_pending = true;
@@ -386,13 +415,21 @@ struct jh_model {
         d_tiles = (AttnTile*)(dm + 2 * t);
         d_mtiles = (AttnTile*)(dm + 2 * t + 5 * tiles.size());
         d_markers = (int32_t*)(dm + 2 * t + 5 * (tiles.size() + mtiles.size()));
-        pairs_global = pairs_local = pairs_marker = 0;
+        d_gtiles = (AttnTile*)(dm + 2 * t + 5 * (tiles.size() + mtiles.size()) + m);
+        nglong = glong;
+        ngshort = gtiles.size() - glong;
+        pairs_global = pairs_local = pairs_marker = pairs_glong = pairs_gshort = rows_glong = 0;
         for (size_t sq = 0; sq < nseq; ++sq) {
             const double n = lens[sq];
             pairs_global += n * n;
+            if (lens[sq] >= kLongSeq) {
+                pairs_glong += n * n;
+                rows_glong += n;
+            }
             const long w = half_window, len = (long)lens[sq];
             for (long i = 0; i < len; ++i) pairs_local += (double)(std::min(i + w, len - 1) - std::max(i - w, 0L) + 1);
         }
+        pairs_gshort = pairs_global - pairs_glong;
         for (const AttnTile& mt : mtiles) pairs_marker += (double)mt.nq * mt.kv_len;
         T = t;
         S = nseq;
@@ -484,11 +521,26 @@ struct jh_model {
     }
 
     void attention(int cls, const bf16_t* q, long ldq, const bf16_t* k, const bf16_t* v, long ldkv, bf16_t* out,
-                   long ldo, const AttnTile* tiles, size_t n, int nheads, int window, double pairs, double qrows) {
-        AttnArgs a{q, ldq, k, v, ldkv, out, ldo, tiles, (int)n, nheads, window, 0.125f * 1.4426950408889634f};
+                   long ldo, const AttnTile* tiles, size_t n, int nheads, int window, double pairs, double qrows,
+                   int waves = 4) {
+        AttnArgs a{q, ldq, k, v, ldkv, out, ldo, tiles, (int)n, nheads, window, 0.125f * 1.4426950408889634f, waves};
         const double hd = 64.0 * nheads;
         timed(cls, 4.0 * hd * pairs, qrows * hd * 2 * 2 + (double)T * hd * 2 * 2, [&] { launch_attention(a, stream); });
         if (profiling && !replay[cls]) replay[cls] = [a, st = stream] { launch_attention(a, st); };
+    }
+
+    // Full attention over every staged sequence (encoder global layers, the
+    // head's full layer): the long sequences' 256-query items, then the rest.
+    void global_attention(int cls, const bf16_t* q, long ldq, const bf16_t* k, const bf16_t* v, long ldkv,
+                          bf16_t* out, long ldo, int nheads) {
+        if (nglong == 0) {
+            attention(cls, q, ldq, k, v, ldkv, out, ldo, d_tiles, ntiles, nheads, -1, pairs_global, (double)T);
+            return;
+        }
+        attention(cls, q, ldq, k, v, ldkv, out, ldo, d_gtiles, nglong, nheads, -1, pairs_glong, rows_glong, 8);
+        if (ngshort > 0)
+            attention(cls, q, ldq, k, v, ldkv, out, ldo, d_gtiles + nglong, ngshort, nheads, -1, pairs_gshort,
+                      (double)T - rows_glong);
     }
 
     void layer_norm(int cls, const float* xp, size_t rows, const float* w, const float* b, float e, bf16_t* out) {
@@ -518,8 +570,7 @@ struct jh_model {
                          nullptr, cos_t, sin_t, 2 * H);
                 const bf16_t* q = qkv.as<bf16_t>();
                 if (L.global)
-                    attention(K_ATTN_GLOBAL, q, 3 * H, q + H, q + 2 * H, 3 * H, ctx.as<bf16_t>(), H, d_tiles, ntiles,
-                              heads, -1, pairs_global, (double)t);
+                    global_attention(K_ATTN_GLOBAL, q, 3 * H, q + H, q + 2 * H, 3 * H, ctx.as<bf16_t>(), H, heads);
                 else
                     attention(K_ATTN_LOCAL, q, 3 * H, q + H, q + 2 * H, 3 * H, ctx.as<bf16_t>(), H, d_tiles, ntiles,
                               heads, half_window, pairs_local, (double)t);
@@ -537,8 +588,7 @@ struct jh_model {
                  ropes[L.rope].first.as<float>(), ropes[L.rope].second.as<float>(), 2 * H, L.wqkv_ws.as<bf16_t>());
             const bf16_t* q = qkv.as<bf16_t>();
             if (L.global)
-                attention(K_ATTN_GLOBAL, q, 3 * H, q + H, q + 2 * H, 3 * H, ctx.as<bf16_t>(), H, d_tiles, ntiles, heads,
-                          -1, pairs_global, (double)t);
+                global_attention(K_ATTN_GLOBAL, q, 3 * H, q + H, q + 2 * H, 3 * H, ctx.as<bf16_t>(), H, heads);
             else
                 attention(K_ATTN_LOCAL, q, 3 * H, q + H, q + 2 * H, 3 * H, ctx.as<bf16_t>(), H, d_tiles, ntiles, heads,
                           half_window, pairs_local, (double)t);
@@ -573,8 +623,7 @@ struct jh_model {
             gemm(K_HEAD_GEMM, JH_EPI_BIAS_BF16, xn.p, H, nullptr, t, L.in_w.as<bf16_t>(), 3 * H, H, qkv.p, 3 * H, 0,
                  L.in_b.as<float>(), nullptr, nullptr, 0, L.in_ws.as<bf16_t>());
             const bf16_t* q = qkv.as<bf16_t>();
-            attention(K_HEAD_ATTN, q, 3 * H, q + H, q + 2 * H, 3 * H, ctx.as<bf16_t>(), H, d_tiles, ntiles, head_heads,
-                      -1, pairs_global, (double)t);
+            global_attention(K_HEAD_ATTN, q, 3 * H, q + H, q + 2 * H, 3 * H, ctx.as<bf16_t>(), H, head_heads);
             gemm_resid_ln(K_HEAD_GEMM, K_HEAD_ROWS, ctx.p, H, t, L.out_w.as<bf16_t>(), H, x.as<float>(),
                           L.out_b.as<float>(), L.norm2_w.as<float>(), L.norm2_b.as<float>(), 1e-5f, xn.as<bf16_t>(),
                           L.out_ws.as<bf16_t>());
@@ -626,14 +675,14 @@ struct jh_model {
             return;
         }
         MetaSlot& ms = slots[cur];
-        const size_t key[6] = {T, M, S, ntiles, nmtiles, (size_t)ws_gen};
-        if (!ms.graph || !std::equal(key, key + 6, ms.graph_key)) {
+        const size_t key[8] = {T, M, S, ntiles, nmtiles, (size_t)ws_gen, nglong, ngshort};
+        if (!ms.graph || !std::equal(key, key + 8, ms.graph_key)) {
             // Capturing and instantiating the ~200-launch forward costs ~0.5 ms
             // on MI355X while replay saves nothing measurable over eager
             // launches, so a shape seen for the first time in a row runs
             // eagerly; the graph is built when the same shape comes again.
-            if (!std::equal(key, key + 6, ms.last_key)) {
-                std::copy(key, key + 6, ms.last_key);
+            if (!std::equal(key, key + 8, ms.last_key)) {
+                std::copy(key, key + 8, ms.last_key);
                 run_all();
                 return;
             }
@@ -660,7 +709,7 @@ struct jh_model {
                 ms.graph = nullptr;
                 throw jh_error(JH_ERR_DEVICE, std::string("hipGraphInstantiate: ") + hipGetErrorString(e));
             }
-            std::copy(key, key + 6, ms.graph_key);
+            std::copy(key, key + 8, ms.graph_key);
         }
         HIP_CHECK(hipGraphLaunch(ms.graph, stream));
     }

@@ -103,6 +103,7 @@ struct AttnArgs {
     int heads;
     int window;        // < 0: global
     float scale_log2;  // softmax scale · log2(e)
+    int waves = 4;     // waves per work item: 4 (tiles of <= 128 queries) or 8 (<= 256 queries)
 };
 
 void launch_attention(const AttnArgs& a, hipStream_t stream);

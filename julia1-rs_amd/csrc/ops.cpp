@@ -142,4 +142,15 @@ int jh_op_attention(const void* q, size_t ldq, const void* k, const void* v, siz
     });
 }
 
+int jh_op_attention_wide(const void* q, size_t ldq, const void* k, const void* v, size_t ldkv, void* out, size_t ldo,
+                         const jh_attn_tile* tiles, size_t ntiles, size_t heads, int window, float scale,
+                         void* stream) {
+    return jh_guarded([&] {
+        AttnArgs a{(const bf16_t*)q, (long)ldq, (const bf16_t*)k, (const bf16_t*)v, (long)ldkv, (bf16_t*)out,
+                   (long)ldo, (const AttnTile*)tiles, as_int(ntiles, "ntiles"), as_int(heads, "heads"), window,
+                   scale * 1.4426950408889634f, 8};
+        launch_attention(a, (hipStream_t)stream);
+    });
+}
+
 }  // extern "C"

@@ -23,7 +23,7 @@ EXPORTS = (
     "jh_op_gemm", "jh_op_gemm_splitk", "jh_op_gemm_splitk_noalloc", "jh_op_gemm_ln", "jh_op_gemm_ws", "jh_op_pack_ws",
     "jh_op_interleave_geglu",
     "jh_op_embed_ln", "jh_op_layer_norm", "jh_op_final_norm",
-    "jh_op_gather_f32", "jh_op_scorer", "jh_op_attention",
+    "jh_op_gather_f32", "jh_op_scorer", "jh_op_attention", "jh_op_attention_wide",
 )
 
 
@@ -88,6 +88,7 @@ def lib():
         L.jh_op_gather_f32.argtypes = [vp, vp, sz, sz, vp, vp]
         L.jh_op_scorer.argtypes = [vp, sz, sz, vp, C.c_float, vp, vp]
         L.jh_op_attention.argtypes = [vp, sz, vp, vp, sz, vp, sz, vp, sz, sz, C.c_int, C.c_float, vp]
+        L.jh_op_attention_wide.argtypes = L.jh_op_attention.argtypes
         _lib = L
     return _lib
 
@@ -311,7 +312,9 @@ def op_scorer(z, w2, b2, out, stream=None):
     check(lib().jh_op_scorer(_dp(z), z.shape[0], z.shape[1], _dp(w2), b2, _dp(out), stream))
 
 
-def op_attention(q, ldq, k, v, ldkv, out, ldo, tiles, heads, window, scale=0.125, stream=None):
-    """q/k/v/out torch bf16 tensors (base pointers of the first row/col); tiles torch int32 [n, 5]."""
-    check(lib().jh_op_attention(_dp(q), ldq, _dp(k), _dp(v), ldkv, _dp(out), ldo, _dp(tiles), tiles.shape[0], heads,
-                                window, scale, stream))
+def op_attention(q, ldq, k, v, ldkv, out, ldo, tiles, heads, window, scale=0.125, stream=None, wide=False):
+    """q/k/v/out torch bf16 tensors (base pointers of the first row/col); tiles torch int32 [n, 5] of at most
+    128 queries each, or 256 with wide=True (eight-wave work items, jh_op_attention_wide)."""
+    fn = lib().jh_op_attention_wide if wide else lib().jh_op_attention
+    check(fn(_dp(q), ldq, _dp(k), _dp(v), ldkv, _dp(out), ldo, _dp(tiles), tiles.shape[0], heads, window, scale,
+             stream))

@@ -326,6 +326,25 @@ def test_base_config3_full_batch(base):
     assert np.abs(full - alone).max() <= 2e-3
 
 
+def test_base_long_and_short_rows(base):
+    """A batch whose global layers take both work-item sizes: two rows of 4096 tokens or more (256-query items of
+    eight waves) and four short rows (128-query items), against the oracle, and each row against itself run
+    alone (where a row of under 4096 tokens takes the 128-query items only)."""
+    ws, gpu, orc = base
+    r = np.random.default_rng(4096)
+    items = []
+    for n in (4100, 130, 4096, 64, 257, 1000):
+        ids = r.integers(0, 50368, size=n, dtype=np.uint32)
+        items.append((ids, [1, n // 2, n - 1], len(items) % 3))
+    b = abi.Batch.from_items(items)
+    full = gpu.forward(b)
+    s = parity(b, full, orc.forward(b))
+    print("long+short", s)
+    check_gates(s)
+    alone = np.concatenate([gpu.forward(b.subset([i])) for i in range(len(items))])
+    assert np.abs(full - alone).max() <= 2e-3
+
+
 def test_profile_replay(tiny):
     """jh_profile_replay times a recorded GEMM/attention launch; staging a batch drops the record."""
     ws, gpu, orc = tiny

@@ -577,6 +577,33 @@ def test_attention_varlen(window, qt):
 
 
 @pytest.mark.parametrize("window", [-1, 64])
+def test_attention_wide_items(window):
+    """jh_op_attention_wide (eight waves, up to 256 queries per work item; the backend's global layers of long
+    sequences) on ragged lengths: each query's keys are visited in the same 64-key tiles as with 128-query items,
+    so the output equals jh_op_attention's bit for bit, and both are within 2e-2 of the f64 reference."""
+    r = rng(31)
+    heads = 2
+    h = heads * 64
+    lens = [1, 100, 129, 255, 256, 257, 511, 700, 1300]
+    t = sum(lens)
+    qkv = bf16_round(r.standard_normal((t, 3 * h), dtype=np.float32))
+    seqs, start = [], 0
+    for ln in lens:
+        seqs.append((start, ln, start, ln, 0))
+        start += ln
+    expect = _attn_ref64(qkv[:, :h], qkv[:, h:2 * h], qkv[:, 2 * h:], seqs, heads, window)
+    dq = dev(qkv, BF16)
+    outs = []
+    for qt, wide in ((128, False), (256, True)):
+        out = torch.zeros(t, h, dtype=BF16, device="cuda")
+        hip.op_attention(dq, 3 * h, dq[:, h:], dq[:, 2 * h:], 3 * h, out, h,
+                         dev(np.array(_tiles(lens, qt), dtype=np.int32)), heads, window, wide=wide)
+        outs.append(host(out))
+    assert np.array_equal(outs[0], outs[1])
+    assert np.abs(outs[1] - expect).max() < 2e-2, np.abs(outs[1] - expect).max()
+
+
+@pytest.mark.parametrize("window", [-1, 64])
 def test_attention_rising_scores(window):
     """Scores that climb along each sequence at several rates (about 2 to 40 log2 units per 64-key tile), so the
     running max must move again and again after the first tile: every rescale case of the online softmax (a rise
