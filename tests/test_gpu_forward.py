@@ -260,6 +260,12 @@ def test_hidden_384_shape(shape):
         s = parity(one, gpu.forward(one), orc.forward(one))
         print(shape, "single request", s)
         check_gates(s)
+        # the reference protocol's longest request (7,556 tokens, src/bin/julia1.rs) with a short row beside it:
+        # the long row's global layers take the 256-query items, the short row's the 128-query ones
+        long = synth.make_batch([7556, 200], [6, 3], cfg.vocab, 19)
+        s = parity(long, gpu.forward(long), orc.forward(long))
+        print(shape, "long request", s)
+        check_gates(s)
 
 
 def test_base_config4_slice(base):
