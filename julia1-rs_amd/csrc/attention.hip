@@ -71,8 +71,8 @@ __device__ constexpr int vswz(int r) { return ((r >> 1) & 1) << 2; }
 // wave meets (a further 1.8% at 4 x 8192).
 template <int NW>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) void attention_kernel(AttnArgs a) {
-    constexpr int RPW = KT / NW;  // K/V rows each wave stages per tile (8 per DMA instruction)
-    constexpr int SPB = NW == 8 ? 2 : 1;  // key tiles staged per barrier
+    constexpr int SPB = NW / 4;           // key tiles staged per barrier
+    constexpr int RPW = SPB * KT / NW;    // K/V rows each wave stages per barrier (8 per DMA instruction)
     __shared__ __align__(1024) bf16_t sK[2 * SPB][KT * 64];
     __shared__ __align__(1024) bf16_t sV[2 * SPB][KT * 64];
 
@@ -111,9 +111,11 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) vo
         kend = min(tile.kv_len, tile.q_pos + tile.nq + a.window);
     }
 
-    // DMA of one K/V tile into buffer `buf`: wave w fills rows [RPW·w, RPW·w+RPW)
-    // of both with RPW/8 1 KB instructions each; lane i of instruction j takes
-    // row RPW·w + 8j + i/8, physical slot i%8.  The lane's byte offsets are
+    // DMA of one stage (SPB K/V tiles, SPB·64 key rows) into stage buffer
+    // `st`: wave w fills rows [RPW·w, RPW·w+RPW) of the stage in both K and V
+    // with RPW/8 1 KB instructions each; lane i of instruction j takes row
+    // RPW·w + 8j + i/8, physical slot i%8 (the swizzles depend on the row
+    // modulo 16, so a row's place inside its 64-row tile decides them).  The lane's byte offsets are
     // fixed per row (the tile adds k0 rows); rows past the sequence end fall
     // outside the buffer resource's range and read as zeros (they are masked
     // to -inf before the softmax, and their zero V rows contribute nothing).
@@ -127,13 +129,13 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) vo
         okb[j] = (uint32_t)(row * a.ldkv + (((lane & 7) ^ kswz(row)) * 8)) * 2;
         ovb[j] = (uint32_t)(row * a.ldkv + (((lane & 7) ^ vswz(row)) * 8)) * 2;
     }
-    auto issue = [&](int k0, int buf) {
-        const uint32_t kt = (uint32_t)(k0 * a.ldkv) * 2;  // bytes of the tile's first key row
+    auto issue = [&](int k0, int st) {
+        const uint32_t kt = (uint32_t)(k0 * a.ldkv) * 2;  // bytes of the stage's first key row
 #pragma unroll
         for (int j = 0; j < RPW / 8; ++j) {
             const int r0 = RPW * wave + 8 * j;
-            const uint32_t lk = __builtin_amdgcn_readfirstlane(lk0 + (buf * KT * 64 + r0 * 64) * 2);
-            const uint32_t lv = __builtin_amdgcn_readfirstlane(lv0 + (buf * KT * 64 + r0 * 64) * 2);
+            const uint32_t lk = __builtin_amdgcn_readfirstlane(lk0 + (st * SPB * KT * 64 + r0 * 64) * 2);
+            const uint32_t lv = __builtin_amdgcn_readfirstlane(lv0 + (st * SPB * KT * 64 + r0 * 64) * 2);
             asm volatile("buffer_load_dwordx4 %1, %2, 0 offen lds" ::"{m0}"(lk), "v"(okb[j] + kt), "s"(rsk)
                          : "memory");
             asm volatile("buffer_load_dwordx4 %1, %2, 0 offen lds" ::"{m0}"(lv), "v"(ovb[j] + kt), "s"(rsv)
@@ -164,22 +166,20 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) vo
     const int qlo = tile.q_pos + wave * 32;
 
     const int ntk = kend > kbeg ? (kend - kbeg + KT - 1) / KT : 0;
-    for (int sub = 0; sub < SPB; ++sub)
-        if (sub < ntk) issue(kbeg + sub * KT, sub);
+    if (ntk > 0) issue(kbeg, 0);
     // A wave with no queries in the tile, or whose 32 queries are all outside
     // the window of a key tile, skips that tile's math (uniform per wave); it
     // still stages its share of K/V and meets every barrier.
     const bool active = wave * 32 < tile.nq;
     for (int it = 0; it < ntk; ++it) {
         const int buf = it % (2 * SPB), k0 = kbeg + it * KT;
-        // tile it landed (this wave's DMA, then everyone's), and every wave is
-        // done with tile it-1, whose buffer the next DMA refills
+        // at a stage's first tile: the stage landed (this wave's DMA, then
+        // everyone's), and every wave is done with the previous stage, whose
+        // buffer the next DMA refills
         if (it % SPB == 0) {
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             __syncthreads();
-#pragma unroll
-            for (int sub = 0; sub < SPB; ++sub)
-                if (it + SPB + sub < ntk) issue(k0 + (SPB + sub) * KT, (it + SPB + sub) % (2 * SPB));
+            if (it + SPB < ntk) issue(k0 + SPB * KT, ((it / SPB) + 1) & 1);
         }
         const bool skip = !active || (a.window >= 0 && (k0 > qlo + 31 + a.window || k0 + KT - 1 < qlo - a.window));
         if (skip) continue;
