@@ -126,6 +126,29 @@ def test_graph_replay_matches_eager(base):
     gpu.set_graph(True)
 
 
+def test_graph_key_tells_long_rows_apart(base):
+    """[4096, 256] and [3968, 384] tokens have the same token, row, marker and 128-query tile counts, but only the
+    first has a row long enough for the global layers' 256-query items. A graph captured for the first must not
+    be replayed for the second: each staged batch's replays equal its eager forward bit for bit."""
+    ws, gpu, _ = base
+    r = np.random.default_rng(7)
+
+    def batch(lens):
+        return abi.Batch.from_items([(r.integers(0, 50368, size=n, dtype=np.uint32), [1, n // 2, n - 1], i % 3)
+                                     for i, n in enumerate(lens)])
+    a, b = batch([4096, 256]), batch([3968, 384])
+    gpu.set_graph(False)
+    eager = [gpu.forward(a), gpu.forward(b)]
+    gpu.set_graph(True)
+    try:
+        for bt, want in ((a, eager[0]), (a, eager[0]), (a, eager[0]), (b, eager[1]), (b, eager[1]), (a, eager[0])):
+            gpu.stage(bt)
+            gpu.execute()
+            assert np.array_equal(gpu.scores(bt.marker_rows.size), want)
+    finally:
+        gpu.set_graph(True)
+
+
 def test_submit_collect_matches_forward(base):
     """jh_submit/jh_collect (pipelined forwards) give jh_forward's scores bit for bit, in any
     collection order; the in-flight limit, double collection and a wrong marker count are errors
