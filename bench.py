@@ -115,6 +115,27 @@ TRAFFIC_SYMBOL = {"gemm_qkv_rope": "gemm_ws_kernel<1>", "gemm_wi_geglu": "gemm_w
                   "gemm_wo2_resid": "gemm_ws2_kernel<36>"}
 
 
+def counter_bytes(rows, copy_mib=256, replays=51):
+    """Bytes per launch of each TRAFFIC_SYMBOL class from one rocprofv3 counter CSV (rows as dicts with
+    Dispatch_Id, Kernel_Name, Counter_Value): the mean over the class's dispatches, leaving out the `replays`
+    kernel dispatches that come last (the bench's back-to-back replays of its dominant launch), scaled so that
+    the three largest copy-kernel dispatches (the --copy-probe copies of `copy_mib` MiB) read as that many bytes.
+    None when there is no such calibration."""
+    rows = sorted(rows, key=lambda r: int(r["Dispatch_Id"]))
+    copies = sorted(float(r["Counter_Value"]) for r in rows if "copyBuffer" in r["Kernel_Name"])[-3:]
+    if len(copies) < 3 or min(copies) <= 0:
+        return None
+    kern = [r for r in rows if "copyBuffer" not in r["Kernel_Name"]]
+    kern = kern[:len(kern) - replays] if replays else kern
+    scale = copy_mib * 1024 * 1024 / statistics.mean(copies)  # counter units -> bytes
+    out = {}
+    for cls, sym in TRAFFIC_SYMBOL.items():
+        vals = [float(r["Counter_Value"]) for r in kern if sym in r["Kernel_Name"]]
+        if vals:
+            out[cls] = statistics.mean(vals) * scale
+    return out
+
+
 def live_traffic(workload):
     """HBM bytes per launch of the TRAFFIC_SYMBOL classes on `workload`, measured in this run: two child runs
     of this bench under `rocprofv3 --pmc` (FETCH_SIZE, then WRITE_SIZE, one counter per run), each value scaled
@@ -150,16 +171,11 @@ def live_traffic(workload):
         if not os.path.exists(path):  # (rocprofv3 may exit 139 after complete results; the file decides)
             return {}, f"{ctr} run gave no counter file (rc {rc})"
         with open(path) as f:
-            rows = sorted(csv.DictReader(f), key=lambda r: int(r["Dispatch_Id"]))
-        copies = sorted(float(r["Counter_Value"]) for r in rows if "copyBuffer" in r["Kernel_Name"])[-3:]
-        kern = [r for r in rows if "copyBuffer" not in r["Kernel_Name"]][:-51]
-        if len(copies) < 3 or min(copies) <= 0:
+            got = counter_bytes(list(csv.DictReader(f)))
+        if got is None:
             return {}, f"{ctr} run has no copy calibration"
-        scale = 256 * 1024 / statistics.mean(copies) * 1024  # counter units -> bytes
-        for cls, sym in TRAFFIC_SYMBOL.items():
-            vals = [float(r["Counter_Value"]) for r in kern if sym in r["Kernel_Name"]]
-            if vals:
-                per.setdefault(cls, {})[ctr] = statistics.mean(vals) * scale
+        for cls, v in got.items():
+            per.setdefault(cls, {})[ctr] = v
     total = {c: int(round(v["FETCH_SIZE"] + v["WRITE_SIZE"])) for c, v in per.items() if len(v) == 2}
     return total, "rocprofv3 --pmc FETCH_SIZE + WRITE_SIZE in two child runs of this bench, copy-calibrated"
 
