@@ -353,6 +353,9 @@ def main():
     # run is itself under a profiler, or a short run without the extra workloads).
     traffic_live, traffic_note = {}, "not measured in this run"
     if not (args.no_extra or args.protocol_only or any(k.startswith("ROCPROF") for k in os.environ)):
+        # Importing torch touches no GPU; doing it here pays a fresh box's first (slow) load of the library
+        # once, before the children's time limits start.
+        import torch  # noqa: F401
         traffic_live, traffic_note = live_traffic(args.workload)
 
     import numpy as np
