@@ -37,6 +37,8 @@
 // branch), which removes most of the 32 rescale multiplies per tile.
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "kernels.hpp"
 
 namespace {
@@ -69,7 +71,7 @@ __device__ constexpr int vswz(int r) { return ((r >> 1) & 1) << 2; }
 // eight-wave form stages two key tiles per barrier (four 16 KB K/V slots,
 // 64 KB: two workgroups per CU still fit), which halves the barriers each
 // wave meets (a further 1.8% at 4 x 8192).
-template <int NW>
+template <int NW, bool WIN>  // WIN: a window layer (a.window >= 0), whose tiles run one 32-key block per step
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) void attention_kernel(AttnArgs a) {
     constexpr int SPB = NW / 4;           // key tiles staged per barrier
     constexpr int RPW = SPB * KT / NW;    // K/V rows each wave stages per barrier (8 per DMA instruction)
@@ -184,16 +186,23 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) vo
         const bool skip = !active || (a.window >= 0 && (k0 > qlo + 31 + a.window || k0 + KT - 1 < qlo - a.window));
         if (skip) continue;
         lds_u8* const vt = (lds_u8*)&sV[buf][0];  // this tile's V buffer
+        // One softmax step over NB 32-key blocks of the tile from block kb0:
+        // the whole tile (NB = 2), or on window layers each block that holds
+        // keys inside the wave's window on its own (NB = 1), which skips the
+        // sixth of a wave's blocks that lie wholly outside it.
+        auto step = [&](auto NBc, const int kb0) {
+        constexpr int NB = decltype(NBc)::value;
+        const int kk0 = k0 + 32 * kb0;  // first key of the step
 
         // Sᵀ for keys [k0, k0+64): two 32-key blocks.
-        auto scores = [&](f32x16(&s)[2]) {
+        auto scores = [&](f32x16(&s)[NB]) {
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
+            for (int kb = 0; kb < NB; ++kb) {
 #pragma unroll
                 for (int e = 0; e < 16; ++e) s[kb][e] = 0.0f;
 #pragma unroll
                 for (int ks = 0; ks < 4; ++ks) {
-                    const int r = kb * 32 + lq;
+                    const int r = (kb0 + kb) * 32 + lq;
                     bf16x8 kf = *(const bf16x8*)&sK[buf][r * 64 + (((ks * 2 + g) ^ kswz(r)) * 8)];
                     s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], s[kb], 0, 0, 0);
                 }
@@ -205,12 +214,12 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) vo
         // pairs would need half the instructions, but on gfx950 it does not
         // issue while an MFMA runs on the SIMD: measured ~7 cycles of MFMA
         // time lost per dot2c, against none for v_add_f32.)
-        uint32_t pp[16];
+        uint32_t pp[8 * NB];
         float ls = 0.0f;
-        auto exps = [&](const f32x16(&s)[2], float mc) {
+        auto exps = [&](const f32x16(&s)[NB], float mc) {
             float part[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
+            for (int kb = 0; kb < NB; ++kb)
 #pragma unroll
                 for (int w = 0; w < 8; ++w) {
                     const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][2 * w], c, -mc));
@@ -224,13 +233,13 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) vo
         // an invalid pair (decided per wave, so the branch is uniform): the
         // sequence end, or a sliding window edge.  Masked scores become -inf,
         // so their p = exp2(-inf) = 0 on either path.
-        const bool tail = k0 + KT > kend;
-        const bool edge = a.window >= 0 && (k0 < qlo + 31 - a.window || k0 + KT - 1 > qlo + a.window);
-        auto mask = [&](f32x16(&s)[2]) {
+        const bool tail = kk0 + 32 * NB > kend;
+        const bool edge = a.window >= 0 && (kk0 < qlo + 31 - a.window || kk0 + 32 * NB - 1 > qlo + a.window);
+        auto mask = [&](f32x16(&s)[NB]) {
             // Element e of block kb is key k0 + kb*32 + (e/4)*8 + 4g + e%4;
             // element offset off (key kl + off) is valid iff lo <= off <= hi:
             // off < kend - kl, and |qpos - kl - off| <= window when windowed.
-            const int kl = k0 + 4 * g;  // key of element 0 in block 0 for this lane
+            const int kl = kk0 + 4 * g;  // key of element 0 in block 0 of the step for this lane
             int lo = 0, hi = kend - kl - 1;
             if (a.window >= 0) {
                 lo = max(lo, qpos - kl - a.window);
@@ -240,7 +249,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) vo
             const unsigned span = hi >= lo ? (unsigned)(hi - lo) : 0u;
             lo = hi >= lo ? lo : 0x40000000;
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
+            for (int kb = 0; kb < NB; ++kb)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
                     const int off = kb * 32 + (e >> 2) * 8 + (e & 3);
@@ -256,19 +265,19 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) vo
         // moves the max.
         bool fast = ref_ok;
         if (fast) {
-            f32x16 s[2];
+            f32x16 s[NB];
             scores(s);
             if (tail || edge) mask(s);
             exps(s, m * c);
             fast = __builtin_amdgcn_ballot_w64(!(ls <= kSumMax)) == 0;
         }
         if (!fast) {
-            f32x16 s[2];
+            f32x16 s[NB];
             scores(s);
             if (tail || edge) mask(s);
             float mx = -INFINITY;
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
+            for (int kb = 0; kb < NB; ++kb)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[kb][e]);
             mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
@@ -295,7 +304,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) vo
         // Oᵀ += Vᵀ·Pᵀ over 4 steps of 16 keys.  Step (kb, hb) uses accumulator
         // elements hb*8 .. hb*8+7 of block kb: keys base + 8*(e/4) + 4g + e%4.
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+        for (int kb = 0; kb < NB; ++kb)
 #pragma unroll
             for (int hb = 0; hb < 2; ++hb) {
                 const bf16x8 pf = __builtin_bit_cast(
@@ -304,7 +313,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) vo
 #pragma unroll
                 for (int db = 0; db < 2; ++db) {
                     // keys kb*32 + hb*16 + 4g + (0..3) and + 8 + (0..3) of dim db*32 + lq
-                    const int at = (int)(db ? voff1 : voff0) + kb * 4096 + hb * 2048;
+                    const int at = (int)(db ? voff1 : voff0) + (kb0 + kb) * 4096 + hb * 2048;
                     const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vt + at));
                     const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vt + at + 1024));
                     const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
@@ -312,6 +321,17 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) vo
                     o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, o[db], 0, 0, 0);
                 }
             }
+        };
+        if constexpr (WIN) {
+#pragma unroll
+            for (int kb0 = 0; kb0 < 2; ++kb0) {
+                const int kk0 = k0 + 32 * kb0;
+                if (kk0 > qlo + 31 + a.window || kk0 + 31 < qlo - a.window) continue;
+                step(std::integral_constant<int, 1>{}, kb0);
+            }
+        } else {
+            step(std::integral_constant<int, 2>{}, 0);
+        }
     }
 
     l += __shfl_xor(l, 32, 64);
@@ -340,7 +360,13 @@ void launch_attention(const AttnArgs& a, hipStream_t s) {
         ((uintptr_t)a.q & 15) || ((uintptr_t)a.k & 15) || ((uintptr_t)a.v & 15) || ((uintptr_t)a.out & 7))
         throw jh_error(1, "attention: operands must be 16-byte aligned with row strides % 8 == 0");
     if ((long)a.ntiles * a.heads > 0x7fffffffL) throw jh_error(1, "attention: grid too large");
-    if (a.waves == 8) JH_LAUNCH(attention_kernel<8>, dim3((unsigned)(a.ntiles * a.heads)), dim3(512), 0, s, a);
-    else JH_LAUNCH(attention_kernel<4>, dim3((unsigned)(a.ntiles * a.heads)), dim3(256), 0, s, a);
+    const dim3 grid((unsigned)(a.ntiles * a.heads));
+    if (a.waves == 8) {
+        if (a.window >= 0) JH_LAUNCH((attention_kernel<8, true>), grid, dim3(512), 0, s, a);
+        else JH_LAUNCH((attention_kernel<8, false>), grid, dim3(512), 0, s, a);
+    } else {
+        if (a.window >= 0) JH_LAUNCH((attention_kernel<4, true>), grid, dim3(256), 0, s, a);
+        else JH_LAUNCH((attention_kernel<4, false>), grid, dim3(256), 0, s, a);
+    }
     HIP_CHECK(hipGetLastError());
 }
